@@ -1,0 +1,227 @@
+/*
+ * supersonic_attn.h — C ABI of the gfx950 (MI355X) full-attention library.
+ *
+ * Two groups of entry points:
+ *
+ *  1. Drop-in replacements for the reference bridge symbols the Rust crate
+ *     `kernel-ffi` binds (crates/kernel-ffi/src/prefill_ffi.rs:635-950).  Same
+ *     names, argument order and meaning, dtype codes, status codes, null
+ *     stream and synchronise-before-return behaviour.
+ *  2. Native fused entry points (`supersonic_attn_gfx950_*`): QK RMSNorm +
+ *     partial RoPE + KV append (bf16 or fp8 e4m3) + split-K / MFMA attention +
+ *     sigmoid gate in one call, asynchronous on a caller stream, over a
+ *     contiguous or block-paged KV cache.
+ *
+ * All pointers are caller-owned device memory unless stated otherwise.  Every
+ * function returns 0 on success and a non-zero status otherwise.
+ */
+#ifndef SUPERSONIC_ATTN_H
+#define SUPERSONIC_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes of ScalarType::kernel_dtype_code (crates/gpu-hal/src/scalar_type.rs:25-32). */
+#define SUPERSONIC_DTYPE_F16 0
+#define SUPERSONIC_DTYPE_F32 1
+#define SUPERSONIC_DTYPE_BF16 2
+/* KV-cache element codes of the native entry points. */
+#define SUPERSONIC_KV_BF16 2
+#define SUPERSONIC_KV_FP8_E4M3 3
+
+/* Status codes of the native entry points (the drop-ins keep the reference's). */
+#define SUPERSONIC_ERR_DTYPE 1001
+#define SUPERSONIC_ERR_HEAD_DIM 1002
+#define SUPERSONIC_ERR_HEADS 1003
+#define SUPERSONIC_ERR_NULL 1004
+#define SUPERSONIC_ERR_ROTARY 1005
+#define SUPERSONIC_ERR_WORKSPACE 1006
+#define SUPERSONIC_ERR_LAUNCH 1007
+#define SUPERSONIC_ERR_SYNC 1008
+#define SUPERSONIC_ERR_RANGE 1009
+#define SUPERSONIC_ERR_CACHE 1010
+
+/* ------------------------------------------------------------------------- */
+/* 1. Drop-in reference symbols                                              */
+/* ------------------------------------------------------------------------- */
+
+/* Causal GQA prefill attention.  Replaces
+ * kernels/full_attention_bridge.cpp:1887 (kernel full_attention.hip:246-361),
+ * bound at crates/kernel-ffi/src/prefill_ffi.rs:899-915.
+ * query [B, Hq, q_len, D], key/value [B, Hkv, kv_len, D] (dtype), out f32
+ * [B, Hq, q_len, D].  Row p attends keys t < min(kv_len, seqlen_offset + p + 1).
+ * dtype 0/1/2.  Status: 64 bad dtype, 14 unsupported head_dim (D > 512 or not
+ * a multiple of 8), 2 workspace allocation, 11 launch, 12 sync. */
+int supersonic_qwen35_hip_full_attention_prefill(
+    int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
+    size_t q_len, size_t kv_len, size_t head_dim, size_t num_kv_groups, float scale,
+    size_t seqlen_offset, const void* query, const void* key, const void* value, void* out);
+
+/* Same contract; replaces kernels/full_attention_bridge_4b.cpp:1906 (no Rust caller). */
+int supersonic_qwen35_4b_hip_full_attention_prefill(
+    int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
+    size_t q_len, size_t kv_len, size_t head_dim, size_t num_kv_groups, float scale,
+    size_t seqlen_offset, const void* query, const void* key, const void* value, void* out);
+
+/* Single-token decode attention.  Replaces kernels/prefill_helpers_bridge.cpp:444-470
+ * (kernel prefill_helpers.hip:319-404), bound at prefill_ffi.rs:917-931.
+ * query [B, Hq, D], key/value [B, Hkv, kv_len, D], out [B, Hq*D] (dtype).
+ * dtype 0/2.  Status: 400 bad dtype, 401 head_dim > 256, 402 launch, 403 sync. */
+int supersonic_qwen35_hip_full_attention_decode_flat(
+    int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
+    size_t kv_len, size_t head_dim, size_t num_kv_groups, float scale,
+    const void* query, const void* key, const void* value, void* out);
+
+/* As decode_flat over a cache whose token capacity kv_stride >= kv_len:
+ * key/value [B, Hkv, kv_stride, D].  Declared at prefill_ffi.rs:934-949; the
+ * reference implements it for CUDA only (full_attention_cuda.cuh:579-680). */
+int supersonic_qwen35_hip_full_attention_decode_flat_strided(
+    int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
+    size_t kv_len, size_t kv_stride, size_t head_dim, size_t num_kv_groups, float scale,
+    const void* query, const void* key, const void* value, void* out);
+
+/* BF16 -> FP8 KV quantiser.  Replaces kernels/full_attention_bridge_4b.cpp:5071-5111
+ * (kernel full_attention_4b.hip:4786-4829), bound at prefill_ffi.rs:856-867.
+ * src [Hkv, seq_len, D] bf16; dst_fp8 [Hkv, max_T, D] u8 and dst_scale
+ * [Hkv, max_T] f32 written at positions pos_offset..pos_offset+seq_len.
+ * Bytes are bit-identical to the reference encoder (float_to_fp8_e4m3,
+ * full_attention_4b.hip:205-232).  dtype 2 only.  Status: 256 bad dtype,
+ * 254 launch, 255 sync. */
+int supersonic_qwen35_4b_hip_quantize_kv_to_fp8(
+    int dtype, size_t device_ordinal, const void* src, void* dst_fp8, float* dst_scale,
+    int num_kv_heads, int seq_len, int head_dim, int max_T, int pos_offset);
+
+/* Row RMSNorm, x * rsqrt(mean(x^2) + eps) * (w [+ 1]).  Replaces
+ * kernels/full_attention_bridge.cpp:3946 (kernel full_attention.hip:2507-2560),
+ * bound at prefill_ffi.rs:637-647.  Status: 74 bad dtype, 71 launch, 72 sync. */
+int supersonic_qwen35_hip_rms_norm(
+    int dtype, size_t device_ordinal, size_t n_rows, size_t n_cols, float eps,
+    int add_unit_offset, const void* xs, const void* weight, void* out);
+
+/* Element cast.  Replaces kernels/full_attention_bridge.cpp:3563, bound at
+ * prefill_ffi.rs:649-656.  Status: 137 bad dtype, 135 launch, 136 sync. */
+int supersonic_qwen35_hip_cast(
+    int input_dtype, int output_dtype, size_t device_ordinal, size_t total_elems,
+    const void* xs, void* out);
+
+/* In-place partial RoPE on [seq_len, num_heads, head_dim]; cos/sin tables
+ * [*, half_rot] already offset to the chunk's first position.  Replaces
+ * kernels/prefill_helpers_bridge.cpp:293 (kernel prefill_helpers.hip:79-108),
+ * bound at prefill_ffi.rs:669-679.  Status: 310 bad dtype, 311 launch, 312 sync. */
+int supersonic_qwen35_hip_apply_rope_prefill(
+    int dtype, size_t device_ordinal, size_t seq_len, size_t num_heads, size_t head_dim,
+    size_t half_rot, const void* cos_table, const void* sin_table, void* data);
+
+/* [S, H, D] -> [H, S, D].  Replaces kernels/prefill_helpers_bridge.cpp:315
+ * (kernel prefill_helpers.hip:114-130), bound at prefill_ffi.rs:681-689.
+ * Status: 320 bad dtype, 321 launch, 322 sync. */
+int supersonic_qwen35_hip_transpose_shd_hsd(
+    int dtype, size_t device_ordinal, size_t s, size_t h, size_t d, const void* src, void* dst);
+
+/* out = data * sigmoid(gate).  Replaces kernels/prefill_helpers_bridge.cpp:363
+ * (kernel prefill_helpers.hip:183-195), bound at prefill_ffi.rs:691-698.
+ * Status: 350 bad dtype, 351 launch, 352 sync. */
+int supersonic_qwen35_hip_sigmoid_mul(
+    int dtype, size_t device_ordinal, size_t total_elems, const void* data, const void* gate,
+    void* out);
+
+/* [S, H, 2D] per-head [q | gate] -> query [S, H, D], gate [S, H, D].  Replaces
+ * kernels/prefill_helpers_bridge.cpp (kernel prefill_helpers.hip:239-257), bound
+ * at prefill_ffi.rs:713-722.  Status: 370 bad dtype, 371 launch, 372 sync. */
+int supersonic_qwen35_hip_split_qgate(
+    int dtype, size_t device_ordinal, size_t s, size_t num_heads, size_t head_dim,
+    const void* src, void* query_out, void* gate_out);
+
+/* ------------------------------------------------------------------------- */
+/* 2. Native fused entry points (no reference counterpart; they replace the  */
+/*    a1-a9 chain of prefill_engine.rs:1951-2308 and the megakernel's        */
+/*    attention phase full_attention_4b.hip:5109-5470)                       */
+/* ------------------------------------------------------------------------- */
+
+/* KV cache view.  Token t of sequence b, kv head h lives at element offset
+ *   contiguous (block_table == NULL):  b*seq_stride + h*head_stride + t*D
+ *   paged:  block_table[b*max_pages_per_seq + t/page_size]*page_stride
+ *           + h*head_stride + (t % page_size)*D
+ * and its fp8 scale (kv_dtype FP8) at the same formula with D = 1 and the
+ * scale_* strides.  The qwen35 crate's [1, Hkv, cap, D] cache per sequence is
+ * contiguous mode with head_stride = cap*D. */
+typedef struct supersonic_kv_cache {
+    void* k;
+    void* v;
+    float* k_scale;
+    float* v_scale;
+    const int32_t* block_table;
+    int64_t seq_stride;
+    int64_t head_stride;
+    int64_t page_stride;
+    int32_t page_size;
+    int32_t max_pages_per_seq;
+    int64_t scale_seq_stride;
+    int64_t scale_head_stride;
+    int64_t scale_page_stride;
+} supersonic_kv_cache;
+
+/* Bytes of workspace supersonic_attn_gfx950_decode needs for this shape. */
+size_t supersonic_attn_gfx950_decode_workspace_size(
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len);
+
+/* One decode step for `batch` sequences: per-head Q/K RMSNorm ((1+w), eps),
+ * partial RoPE at positions[b], append K/V at slot positions[b] (fp8: per
+ * (token, head) absmax scale, OCP e4m3), split-K attention over slots
+ * 0..positions[b] (the new token read unquantised), sigmoid gate.
+ * q_proj [batch, Hq*2D] bf16 (per head [q | gate]); k_new, v_new [batch, Hkv*D]
+ * bf16; q_norm_w, k_norm_w [D] bf16; cos/sin [max_pos, rotary_dim/2] bf16;
+ * positions [batch] int32 device; out [batch, Hq*D] bf16.  max_kv_len >=
+ * max(positions)+1.  workspace may be NULL (library-owned).  Asynchronous on
+ * `stream` (hipStream_t; NULL = null stream). */
+int supersonic_attn_gfx950_decode(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
+    size_t max_kv_len, float eps, float scale,
+    const void* q_proj, const void* k_new, const void* v_new,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const int32_t* positions, const supersonic_kv_cache* cache, void* out,
+    void* workspace, size_t workspace_bytes);
+
+/* Attention-only decode over an existing cache: q [batch, Hq, D] bf16 (already
+ * normalised and rotated), kv_lens [batch] int32 device, optional gate
+ * [batch, Hq*D] bf16 (NULL = no gate), out [batch, Hq*D] bf16. */
+int supersonic_attn_gfx950_decode_attend(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len,
+    float scale, const void* q, const int32_t* kv_lens, const supersonic_kv_cache* cache,
+    const void* gate, void* out, void* workspace, size_t workspace_bytes);
+
+/* One prefill chunk of one sequence (cache sequence index 0): tokens at
+ * positions chunk_start .. chunk_start+chunk_len-1.  Q/K RMSNorm + RoPE, K/V
+ * written to the cache (bf16, or fp8 with scales), causal MFMA attention over
+ * the cached prefix plus the chunk, sigmoid gate.  q_proj [S, Hq*2D],
+ * k_new/v_new [S, Hkv*D], out [S, Hq*D], all bf16.  Asynchronous on `stream`. */
+int supersonic_attn_gfx950_prefill(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
+    size_t chunk_len, size_t chunk_start, float eps, float scale,
+    const void* q_proj, const void* k_new, const void* v_new,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const supersonic_kv_cache* cache, void* out);
+
+/* OCP e4m3 variant of supersonic_qwen35_4b_hip_quantize_kv_to_fp8: same
+ * layout and scale rule (scale = max(absmax/448, 1e-12)), hardware OCP
+ * round-to-nearest-even codes, the codec the fused entry points write.
+ * Asynchronous on `stream`. */
+int supersonic_attn_gfx950_quantize_kv_fp8_ocp(
+    size_t device_ordinal, void* stream, const void* src, void* dst_fp8, float* dst_scale,
+    int num_kv_heads, int seq_len, int head_dim, int max_T, int pos_offset);
+
+/* Library version string. */
+const char* supersonic_attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUPERSONIC_ATTN_H */

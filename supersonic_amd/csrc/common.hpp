@@ -1,0 +1,183 @@
+// Shared device/host helpers for the gfx950 full-attention library.
+// CDNA4 only: wave64, MFMA, OCP e4m3 hardware converts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace ssa {
+
+// ----------------------------------------------------------------------------
+// Scalar element types.  bf16 / f16 are carried as raw 16-bit patterns so the
+// kernels control every rounding step themselves.
+// ----------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+typedef float f32x16_v __attribute__((ext_vector_type(16)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even f32 -> bf16 bits (finite inputs; NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu)) return (u >> 16) | 0x40u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ float bf16_round(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+    _Float16 h;
+    uint16_t s = static_cast<uint16_t>(b);
+    __builtin_memcpy(&h, &s, 2);
+    return static_cast<float>(h);
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
+    _Float16 h = static_cast<_Float16>(x);
+    uint16_t s;
+    __builtin_memcpy(&s, &h, 2);
+    return s;
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<bf16_t> {
+    static __device__ __forceinline__ float to_f32(uint32_t b) { return bf16_bits_to_f32(b); }
+    static __device__ __forceinline__ uint32_t from_f32(float x) { return f32_to_bf16_bits(x); }
+};
+template <> struct Elem<f16_t> {
+    static __device__ __forceinline__ float to_f32(uint32_t b) { return f16_bits_to_f32(b); }
+    static __device__ __forceinline__ uint32_t from_f32(float x) { return f32_to_f16_bits(x); }
+};
+
+template <typename T> __device__ __forceinline__ float load_f32(const T* p, size_t i);
+template <> __device__ __forceinline__ float load_f32<float>(const float* p, size_t i) { return p[i]; }
+template <> __device__ __forceinline__ float load_f32<bf16_t>(const bf16_t* p, size_t i) { return bf16_bits_to_f32(p[i].bits); }
+template <> __device__ __forceinline__ float load_f32<f16_t>(const f16_t* p, size_t i) { return f16_bits_to_f32(p[i].bits); }
+
+template <typename T> __device__ __forceinline__ void store_f32(T* p, size_t i, float x);
+template <> __device__ __forceinline__ void store_f32<float>(float* p, size_t i, float x) { p[i] = x; }
+template <> __device__ __forceinline__ void store_f32<bf16_t>(bf16_t* p, size_t i, float x) { p[i].bits = static_cast<uint16_t>(f32_to_bf16_bits(x)); }
+template <> __device__ __forceinline__ void store_f32<f16_t>(f16_t* p, size_t i, float x) { p[i].bits = static_cast<uint16_t>(f32_to_f16_bits(x)); }
+
+// Unpack 8 packed 16-bit values (a 16-byte load) to f32.
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4_v& w, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = Elem<T>::to_f32(w[i] & 0xFFFFu);
+        f[2 * i + 1] = Elem<T>::to_f32(w[i] >> 16);
+    }
+}
+template <>
+__device__ __forceinline__ void unpack8<bf16_t>(const u32x4_v& w, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// OCP e4m3 through the gfx950 converters.
+// ----------------------------------------------------------------------------
+// Two e4m3 bytes (selected by word_hi: bytes 0-1 or 2-3 of v) -> 2 floats.
+__device__ __forceinline__ f32x2_v fp8x2_to_f32(uint32_t v, bool word_hi) {
+    return word_hi ? __builtin_amdgcn_cvt_pk_f32_fp8(v, true) : __builtin_amdgcn_cvt_pk_f32_fp8(v, false);
+}
+// Four floats -> four e4m3 bytes, round-to-nearest-even, saturated to +-448.
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4(float a, float b, float c, float d) {
+    a = fminf(fmaxf(a, -448.f), 448.f);
+    b = fminf(fmaxf(b, -448.f), 448.f);
+    c = fminf(fmaxf(c, -448.f), 448.f);
+    d = fminf(fmaxf(d, -448.f), 448.f);
+    uint32_t r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0u, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+    return r;
+}
+
+// ----------------------------------------------------------------------------
+// Cross-lane reductions.  DPP row rotates stay inside 16-lane rows.
+// ----------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Reduce across the 16 lanes of each DPP row; every lane gets the result.
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f32<0x128>(x));  // row_ror:8
+    x = fmaxf(x, dpp_f32<0x124>(x));  // row_ror:4
+    x = fmaxf(x, dpp_f32<0x122>(x));  // row_ror:2
+    x = fmaxf(x, dpp_f32<0x121>(x));  // row_ror:1
+    return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f32<0x128>(x);
+    x += dpp_f32<0x124>(x);
+    x += dpp_f32<0x122>(x);
+    x += dpp_f32<0x121>(x);
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row16_sum(x);
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+    x = row16_max(x);
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+
+__device__ __forceinline__ u32x4_v ld16(const void* p) {
+    return *reinterpret_cast<const u32x4_v*>(p);
+}
+__device__ __forceinline__ void st16(void* p, const u32x4_v& v) {
+    *reinterpret_cast<u32x4_v*>(p) = v;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace ssa
+
+// ----------------------------------------------------------------------------
+// Host side
+// ----------------------------------------------------------------------------
+namespace ssa {
+
+// Saves, sets and restores the current device around a bridge call, the
+// reference bridges' ScopedHipDevice (kernels/prefill_helpers_bridge.cpp:11-19).
+struct ScopedDevice {
+    int previous = -1;
+    bool changed = false;
+    explicit ScopedDevice(int target) {
+        if (hipGetDevice(&previous) != hipSuccess) previous = -1;
+        if (previous != target) {
+            if (hipSetDevice(target) == hipSuccess) changed = true;
+        }
+    }
+    ~ScopedDevice() {
+        if (changed && previous >= 0) (void)hipSetDevice(previous);
+    }
+};
+
+// Per-device scratch owned by the library: grown on demand, never shrunk,
+// released at process exit.  Used for split-K partials of the entry points
+// that have no workspace argument.
+void* device_workspace(int device, size_t bytes);
+
+inline unsigned grid1d(size_t n, int block) {
+    return static_cast<unsigned>((n + block - 1) / block);
+}
+
+}  // namespace ssa

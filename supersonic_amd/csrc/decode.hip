@@ -1,0 +1,827 @@
+// Split-K GQA decode attention for gfx950.
+//
+// Replaces the reference's decode attention cores:
+//   * pfx_full_attention_decode_flat_kernel  kernels/prefill_helpers.hip:319-404
+//     (one 32-lane block per query head, K read twice, serial over tokens);
+//   * the megakernel attention phase        kernels/full_attention_4b.hip:5109-5470
+//     (QK-norm, RoPE, KV append, FP8 quantise, online softmax, gate; block 0
+//     of the whole grid, two barriers per token).
+//
+// Design (HBM-bound; every K/V byte is read exactly once):
+//   grid  = (split, kv_head, batch); a workgroup owns `chunk` consecutive tokens
+//           of one kv head and serves all G = Hq/Hkv query heads that share it.
+//   block = 4 wave64s; wave w takes the 16-token blocks w, w+4, ... of the chunk.
+//   QK^T  : v_mfma_f32_16x16x32_{bf16,f16}.  A = the G query heads (rows, zero
+//           padded to 16), B = 16 tokens of K loaded straight from HBM in the
+//           B-operand layout (16 B per lane per k-step).  The score tile lands
+//           with one token per lane of each 16-lane DPP row, so softmax row
+//           statistics are 4 DPP row_ror steps.
+//   softmax: online, base 2, per head; per-lane partial sums reduced once.
+//   PV    : VALU; each lane owns 8 dims of one token (128-bit loads), P is
+//           broadcast through a per-wave LDS tile.
+//   merge : the 4 waves merge through LDS; splits merge in a second kernel
+//           (log-sum-exp), which also applies the sigmoid gate.
+//   FP8   : e4m3 bytes -> bf16 with the hardware OCP converter; the per-token
+//           K scale multiplies the score, the V scale multiplies p.
+//   Fused prologue: the workgroup normalises + rotates its q heads; the split
+//           that owns the new token also normalises + rotates k, writes K/V
+//           (or fp8 codes + scales) into the cache and reads the new token from
+//           LDS, unquantised (as full_attention_4b.hip:5351-5353 does).
+#include <cstdlib>
+#include <mutex>
+#include <utility>
+#include <vector>
+
+#include "common.hpp"
+#include "kv_view.hpp"
+
+namespace ssa {
+
+struct DecodeParams {
+    KvView kv;
+    const uint16_t* q;        // attend: q [B, Hq, D]; fused: q_proj [B, Hq*2D]
+    int64_t q_bstride;        // elements between batch rows of q
+    int64_t q_hstride;        // elements between heads of q
+    const int32_t* lens;      // kv_lens [B] (attend) or positions [B] (fused)
+    int len_plus;             // 0 (attend) or 1 (fused: len = position + 1)
+    int Hq, Hkv, G, chunk, nsplit;
+    float scale_log2;         // softmax scale * log2(e)
+    int fused;
+    const uint16_t* k_new;    // [B, Hkv*D] bf16
+    const uint16_t* v_new;
+    const uint16_t* q_norm_w; // [D] bf16
+    const uint16_t* k_norm_w;
+    const uint16_t* cos_t;    // [max_pos, half_rot] bf16
+    const uint16_t* sin_t;
+    int half_rot;
+    float eps;
+    float* part_o;            // [B, Hq, nsplit, D]
+    float* part_ml;           // [B, Hq, nsplit, 2] (max in log2 units, sum)
+};
+
+template <typename QT> struct Mfma;
+template <> struct Mfma<bf16_t> {
+    typedef bf16x8_v op;
+    static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma<f16_t> {
+    typedef f16x8_v op;
+    static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <typename OP>
+__device__ __forceinline__ OP as_op(const u32x4_v& w) {
+    OP r;
+    __builtin_memcpy(&r, &w, 16);
+    return r;
+}
+
+// 8 e4m3 bytes -> 8 bf16 (exact: every e4m3 value is a bf16 value).
+__device__ __forceinline__ u32x4_v fp8x8_to_bf16x8(u32x2_v w) {
+    u32x4_v r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        f32x2_v lo = fp8x2_to_f32(w[i], false);
+        f32x2_v hi = fp8x2_to_f32(w[i], true);
+        r[2 * i] = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u);
+        r[2 * i + 1] = __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u);
+    }
+    return r;
+}
+
+__device__ __forceinline__ void fp8x8_to_f32(u32x2_v w, float* f) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        f32x2_v lo = fp8x2_to_f32(w[i], false);
+        f32x2_v hi = fp8x2_to_f32(w[i], true);
+        f[4 * i + 0] = lo[0];
+        f[4 * i + 1] = lo[1];
+        f[4 * i + 2] = hi[0];
+        f[4 * i + 3] = hi[1];
+    }
+}
+
+template <typename QT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);
+}
+
+template <typename QT, bool FP8, int D, int GP>
+__global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
+    static_assert(D % 64 == 0 && D <= 512, "head_dim");
+    static_assert(GP == 4 || GP == 8 || GP == 16, "padded group");
+    typedef typename Mfma<QT>::op op_t;
+    constexpr int KSTEPS = D / 32;
+    constexpr int LPT = D / 8;       // lanes per token row in the V layout
+    constexpr int TPI = 64 / LPT;    // tokens per V load instruction
+    constexpr int VINS = 16 / TPI;   // V load instructions per 16-token block
+    constexpr int ESZ = FP8 ? 1 : 2;
+
+    __shared__ float smem[2 * GP * D];         // q staging, then the wave merge
+    __shared__ float p_s[4][16][GP];           // per-wave probabilities
+    __shared__ float kn_s[D], vn_s[D];         // the new token (fused owner split)
+    __shared__ float ml_s[4][GP][2];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int len = p.lens[b] + p.len_plus;
+    const int t_begin = split * p.chunk;
+    if (t_begin >= len) return;  // uniform: ragged batch, nothing to do
+    const int t_end = min(len, t_begin + p.chunk);
+    const int G = p.G;
+    const int pos = len - 1;
+    const bool owner = p.fused && pos >= t_begin && pos < t_end;
+
+    // ---------------------------------------------------------------- prologue
+    for (int idx = tid; idx < GP * D; idx += 256) {
+        const int h = idx / D, d = idx % D;
+        float x = 0.f;
+        if (h < G) x = Elem<QT>::to_f32(p.q[b * p.q_bstride + (kvh * G + h) * p.q_hstride + d]);
+        smem[idx] = x;
+    }
+    if (owner) {
+        for (int d = tid; d < D; d += 256) {
+            const int64_t o = (static_cast<int64_t>(b) * p.Hkv + kvh) * D + d;
+            kn_s[d] = bf16_bits_to_f32(p.k_new[o]);
+            vn_s[d] = bf16_bits_to_f32(p.v_new[o]);
+        }
+    }
+    __syncthreads();
+    if (p.fused) {
+        // Per-head RMSNorm with (1 + w), bf16 result (full_attention_4b.hip:5142-5191).
+        const int rows = G + (owner ? 1 : 0);
+        for (int r = wave; r < rows; r += 4) {
+            float* row = r < G ? &smem[r * D] : kn_s;
+            const uint16_t* w = r < G ? p.q_norm_w : p.k_norm_w;
+            float ss = 0.f;
+            for (int d = lane; d < D; d += 64) ss += row[d] * row[d];
+            ss = wave_sum(ss);
+            const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
+            for (int d = lane; d < D; d += 64)
+                row[d] = bf16_round(row[d] * inv * (bf16_bits_to_f32(w[d]) + 1.0f));
+        }
+        __syncthreads();
+        // Rotate-half partial RoPE at the new token's position (:5193-5224).
+        const int hr = p.half_rot;
+        if (hr > 0) {
+            const uint16_t* ct = p.cos_t + static_cast<int64_t>(pos) * hr;
+            const uint16_t* st = p.sin_t + static_cast<int64_t>(pos) * hr;
+            for (int idx = tid; idx < rows * hr; idx += 256) {
+                const int r = idx / hr, i = idx % hr;
+                float* row = r < G ? &smem[r * D] : kn_s;
+                const float c = bf16_bits_to_f32(ct[i]), s = bf16_bits_to_f32(st[i]);
+                const float x0 = row[i], x1 = row[i + hr];
+                row[i] = bf16_round(x0 * c - x1 * s);
+                row[i + hr] = bf16_round(x0 * s + x1 * c);
+            }
+        }
+        __syncthreads();
+        // KV append at slot pos (:5226-5296); FP8 uses the absmax scale and OCP e4m3.
+        if (owner) {
+            const int64_t off = p.kv.row(b, kvh, pos, D);
+            if constexpr (!FP8) {
+                uint16_t* kc = reinterpret_cast<uint16_t*>(p.kv.k) + off;
+                uint16_t* vc = reinterpret_cast<uint16_t*>(p.kv.v) + off;
+                for (int d = tid; d < D; d += 256) {
+                    kc[d] = static_cast<uint16_t>(f32_to_bf16_bits(kn_s[d]));
+                    vc[d] = static_cast<uint16_t>(f32_to_bf16_bits(vn_s[d]));
+                }
+            } else {
+                if (wave < 2) {
+                    const float* src = wave == 0 ? kn_s : vn_s;
+                    uint8_t* dst = (wave == 0 ? p.kv.k : p.kv.v) + off;
+                    float am = 0.f;
+                    for (int d = lane; d < D; d += 64) am = fmaxf(am, fabsf(src[d]));
+                    am = wave_max(am);
+                    const float sc = fmaxf(am / 448.0f, 1e-12f);
+                    const float inv = 1.0f / sc;
+                    for (int d = lane * 4; d < D; d += 256) {
+                        const uint32_t c4 = f32x4_to_fp8x4(src[d] * inv, src[d + 1] * inv,
+                                                           src[d + 2] * inv, src[d + 3] * inv);
+                        *reinterpret_cast<uint32_t*>(dst + d) = c4;
+                    }
+                    if (lane == 0) (wave == 0 ? p.kv.ks : p.kv.vs)[p.kv.srow(b, kvh, pos)] = sc;
+                }
+            }
+        }
+    }
+
+    // Q as the MFMA A operand: row = head (lane & 15), k = dims 32s + 8(lane>>4) + j.
+    op_t qa[KSTEPS];
+    {
+        const int hh = lane & 15;
+        const int dk = 8 * (lane >> 4);
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            u32x4_v w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float a = 0.f, c = 0.f;
+                if (hh < G) {
+                    a = smem[hh * D + 32 * s + dk + 2 * j];
+                    c = smem[hh * D + 32 * s + dk + 2 * j + 1];
+                }
+                w[j] = pack2<QT>(a, c);
+            }
+            qa[s] = as_op<op_t>(w);
+        }
+    }
+    __syncthreads();  // smem is reused by the merge below
+
+    // ---------------------------------------------------------------- main loop
+    float m[4], lsum[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m[i] = -1e30f; lsum[i] = 0.f; }
+    float acc[GP][8];
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+
+    const int n_s = lane & 15;           // score lane: token within the block
+    const int vt = lane / LPT;           // V lane: token within the instruction
+    const int vd = (lane % LPT) * 8;     // V lane: first dim
+    const int nblk = (t_end - t_begin + 15) >> 4;
+    const uint8_t* kbase = p.kv.k;
+    const uint8_t* vbase = p.kv.v;
+
+    for (int blk = wave; blk < nblk; blk += 4) {
+        const int t0 = t_begin + blk * 16;
+        const int64_t base = p.kv.row(b, kvh, t0, D);  // block lies inside one page
+        const int last = len - 1 - t0;                  // clamp loads to live rows
+
+        // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
+        op_t kb[KSTEPS];
+        {
+            const int kn = min(n_s, last);
+            const uint8_t* kp = kbase + (base + static_cast<int64_t>(kn) * D + 8 * (lane >> 4)) * ESZ;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                if constexpr (!FP8) {
+                    kb[s] = as_op<op_t>(ld16(kp + 64 * s));
+                } else {
+                    kb[s] = as_op<op_t>(fp8x8_to_bf16x8(*reinterpret_cast<const u32x2_v*>(kp + 32 * s)));
+                }
+            }
+        }
+        // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
+        u32x4_v vr16[FP8 ? 1 : VINS];
+        u32x2_v vr8[FP8 ? VINS : 1];
+#pragma unroll
+        for (int j = 0; j < VINS; ++j) {
+            const int tk = min(TPI * j + vt, last);
+            const uint8_t* vp = vbase + (base + static_cast<int64_t>(tk) * D + vd) * ESZ;
+            if constexpr (!FP8) vr16[j] = ld16(vp);
+            else vr8[j] = *reinterpret_cast<const u32x2_v*>(vp);
+        }
+        float ksc = 1.f, vsc = 1.f;
+        if constexpr (FP8) {
+            const int64_t sb = p.kv.srow(b, kvh, t0);
+            const int kn = min(n_s, last);
+            ksc = p.kv.ks[sb + kn];
+            vsc = p.kv.vs[sb + kn];
+        }
+        const bool has_new = owner && pos >= t0 && pos < t0 + 16;
+        if (has_new && n_s == pos - t0) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                u32x4_v w;
+                const int d0 = 32 * s + 8 * (lane >> 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(kn_s[d0 + 2 * j], kn_s[d0 + 2 * j + 1]);
+                kb[s] = as_op<op_t>(w);
+            }
+            ksc = 1.f;
+            vsc = 1.f;
+        }
+
+        f32x4_v sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) sc = Mfma<QT>::mma(qa[s], kb[s], sc);
+
+        const bool valid = (t0 + n_s) < t_end;
+        float pr[4], al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float s2 = valid ? sc[i] * (p.scale_log2 * ksc) : -INFINITY;
+            const float bm = row16_max(s2);
+            const float mn = fmaxf(m[i], bm);
+            al[i] = exp2f(m[i] - mn);
+            const float pe = exp2f(s2 - mn);
+            lsum[i] = lsum[i] * al[i] + pe;
+            m[i] = mn;
+            pr[i] = pe * vsc;
+        }
+        if (4 * (lane >> 4) < GP) {
+            f32x4_v pv = {pr[0], pr[1], pr[2], pr[3]};
+            *reinterpret_cast<f32x4_v*>(&p_s[wave][n_s][4 * (lane >> 4)]) = pv;
+        }
+        float alpha[GP];
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+            alpha[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[h & 3]), 16 * (h >> 2)));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
+
+#pragma unroll
+        for (int j = 0; j < VINS; ++j) {
+            const int tn = TPI * j + vt;
+            float vf[8];
+            if constexpr (!FP8) unpack8<QT>(vr16[j], vf);
+            else fp8x8_to_f32(vr8[j], vf);
+            if (has_new && tn == pos - t0) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vf[e] = vn_s[vd + e];
+            }
+            float pv[GP];
+#pragma unroll
+            for (int h4 = 0; h4 < GP / 4; ++h4) {
+                const f32x4_v t = *reinterpret_cast<const f32x4_v*>(&p_s[wave][tn][4 * h4]);
+                pv[4 * h4] = t[0];
+                pv[4 * h4 + 1] = t[1];
+                pv[4 * h4 + 2] = t[2];
+                pv[4 * h4 + 3] = t[3];
+            }
+#pragma unroll
+            for (int h = 0; h < GP; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pv[h], vf[e], acc[h][e]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---------------------------------------------------------------- merge
+    float ltot[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1)
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
+
+    if ((lane & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = 4 * (lane >> 4) + i;
+            if (h < GP) {
+                ml_s[wave][h][0] = m[i];
+                ml_s[wave][h][1] = ltot[i];
+            }
+        }
+    }
+    __syncthreads();
+    float fw[GP];
+#pragma unroll
+    for (int h = 0; h < GP; ++h) {
+        float M = fmaxf(fmaxf(ml_s[0][h][0], ml_s[1][h][0]), fmaxf(ml_s[2][h][0], ml_s[3][h][0]));
+        fw[h] = exp2f(ml_s[wave][h][0] - M);
+    }
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
+
+    // Two LDS rounds: waves 2,3 -> 0,1, then wave 1 -> 0.
+    if (wave >= 2 && lane < LPT) {
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) smem[((wave - 2) * GP + h) * D + vd + e] = acc[h][e];
+    }
+    __syncthreads();
+    if (wave < 2 && lane < LPT) {
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] += smem[(wave * GP + h) * D + vd + e];
+    }
+    __syncthreads();
+    if (wave == 1 && lane < LPT) {
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) smem[h * D + vd + e] = acc[h][e];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        if (lane < LPT) {
+#pragma unroll
+            for (int h = 0; h < GP; ++h) {
+                if (h < G) {
+                    float o[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] = acc[h][e] + smem[h * D + vd + e];
+                    const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
+                    float* dst = p.part_o + row * D + vd;
+                    f32x4_v o0 = {o[0], o[1], o[2], o[3]}, o1 = {o[4], o[5], o[6], o[7]};
+                    *reinterpret_cast<f32x4_v*>(dst) = o0;
+                    *reinterpret_cast<f32x4_v*>(dst + 4) = o1;
+                }
+            }
+        }
+        if (lane < G) {
+            const int h = lane;
+            float M = -1e30f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) M = fmaxf(M, ml_s[w][h][0]);
+            float L = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) L += exp2f(ml_s[w][h][0] - M) * ml_s[w][h][1];
+            const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
+            p.part_ml[2 * row] = M;
+            p.part_ml[2 * row + 1] = L;
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Split merge + output cast + optional sigmoid gate.
+// grid = (Hq, B, D/64), block = 64.
+// ----------------------------------------------------------------------------
+struct MergeParams {
+    const float* part_o;
+    const float* part_ml;
+    const int32_t* lens;
+    int len_plus;
+    int Hq, D, chunk, nsplit;
+    const uint16_t* gate;     // NULL, or gate element (b, h, d) at b*g_bstride + h*g_hstride + d
+    int64_t g_bstride, g_hstride;
+    void* out;                // [B, Hq*D] of OT
+};
+
+template <typename OT>
+__global__ __launch_bounds__(64) void decode_merge_kernel(MergeParams p) {
+    __shared__ float f_s[1024];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int d = blockIdx.z * 64 + threadIdx.x;
+    const int len = p.lens[b] + p.len_plus;
+    const int ns = len > 0 ? (len + p.chunk - 1) / p.chunk : 0;
+    const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + h) * p.nsplit;
+    float M = -1e30f;
+    for (int s = threadIdx.x; s < ns; s += 64) M = fmaxf(M, p.part_ml[2 * (row0 + s)]);
+    M = wave_max(M);
+    float L = 0.f;
+    for (int s = threadIdx.x; s < ns; s += 64) {
+        const float f = exp2f(p.part_ml[2 * (row0 + s)] - M);
+        f_s[s] = f;
+        L += f * p.part_ml[2 * (row0 + s) + 1];
+    }
+    L = wave_sum(L);
+    __syncthreads();
+    float o = 0.f;
+    for (int s = 0; s < ns; ++s) o = fmaf(f_s[s], p.part_o[(row0 + s) * p.D + d], o);
+    float r = L > 0.f ? o / L : 0.f;
+    const int64_t oi = (static_cast<int64_t>(b) * p.Hq + h) * p.D + d;
+    if (p.gate) {
+        const float g = bf16_bits_to_f32(p.gate[b * p.g_bstride + h * p.g_hstride + d]);
+        r = bf16_round(bf16_round(r) * (1.0f / (1.0f + expf(-g))));
+    }
+    store_f32(static_cast<OT*>(p.out), oi, r);
+}
+
+// ----------------------------------------------------------------------------
+// Host launch
+// ----------------------------------------------------------------------------
+struct SplitPlan {
+    int chunk;
+    int nsplit;
+};
+
+static int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    if (!v || !*v) return dflt;
+    return atoi(v);
+}
+
+// Chunk of tokens per workgroup: enough workgroups to fill 256 CUs a few
+// times over, but chunks of at least 64 tokens (4 waves x 16).
+static SplitPlan plan_splits(int B, int Hkv, int max_len) {
+    const int target = env_int("SUPERSONIC_DECODE_TARGET_WGS", 1024);
+    const int min_chunk = env_int("SUPERSONIC_DECODE_MIN_CHUNK", 128);
+    const int pairs = B * Hkv;
+    int want = (target + pairs - 1) / pairs;
+    if (want < 1) want = 1;
+    int chunk = (max_len + want - 1) / want;
+    chunk = ((chunk + 63) / 64) * 64;
+    if (chunk < min_chunk) chunk = min_chunk;
+    int nsplit = (max_len + chunk - 1) / chunk;
+    if (nsplit > 1024) {  // the merge kernel stages at most 1024 split weights
+        chunk = ((max_len + 1023) / 1024 + 63) / 64 * 64;
+        nsplit = (max_len + chunk - 1) / chunk;
+    }
+    if (nsplit < 1) nsplit = 1;
+    return {chunk, nsplit};
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+static size_t workspace_bytes_for(int B, int Hq, int D, int nsplit) {
+    const size_t rows = static_cast<size_t>(B) * Hq * nsplit;
+    return align256(rows * D * sizeof(float)) + align256(rows * 2 * sizeof(float));
+}
+
+template <typename QT, bool FP8, int D>
+static hipError_t launch_split(dim3 grid, hipStream_t st, int GP, const DecodeParams& p) {
+    switch (GP) {
+    case 4: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 4>), grid, dim3(256), 0, st, p); break;
+    case 8: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 8>), grid, dim3(256), 0, st, p); break;
+    default: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 16>), grid, dim3(256), 0, st, p); break;
+    }
+    return hipGetLastError();
+}
+
+template <typename QT, bool FP8>
+static hipError_t launch_split_d(int D, dim3 grid, hipStream_t st, int GP, const DecodeParams& p) {
+    switch (D) {
+    case 64: return launch_split<QT, FP8, 64>(grid, st, GP, p);
+    case 128: return launch_split<QT, FP8, 128>(grid, st, GP, p);
+    case 256: return launch_split<QT, FP8, 256>(grid, st, GP, p);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+struct DecodeRequest {
+    int qdtype;       // 0 f16, 2 bf16
+    bool fp8;
+    int B, Hq, Hkv, D;
+    int max_len;
+    float scale;
+    DecodeParams prm;         // q/lens/fused fields filled by the caller
+    const uint16_t* gate;
+    int64_t g_bstride, g_hstride;
+    void* out;
+    void* workspace;
+    size_t workspace_bytes;
+    int device;
+    hipStream_t stream;
+};
+
+// Returns 0, or a SUPERSONIC_ERR_* status.
+static int run_decode(DecodeRequest& r) {
+    if (r.D != 64 && r.D != 128 && r.D != 256) return SUPERSONIC_ERR_HEAD_DIM;
+    if (r.Hkv <= 0 || r.Hq % r.Hkv != 0) return SUPERSONIC_ERR_HEADS;
+    const int G = r.Hq / r.Hkv;
+    if (G > 16) return SUPERSONIC_ERR_HEADS;
+    const int GP = G <= 4 ? 4 : (G <= 8 ? 8 : 16);
+    if (r.B <= 0) return 0;
+    if (r.max_len <= 0) r.max_len = 1;
+    const SplitPlan sp = plan_splits(r.B, r.Hkv, r.max_len);
+    const size_t need = workspace_bytes_for(r.B, r.Hq, r.D, sp.nsplit);
+    void* ws = r.workspace;
+    if (ws) {
+        if (r.workspace_bytes < need) return SUPERSONIC_ERR_WORKSPACE;
+    } else {
+        ws = device_workspace(r.device, need);
+        if (!ws) return SUPERSONIC_ERR_WORKSPACE;
+    }
+    const size_t rows = static_cast<size_t>(r.B) * r.Hq * sp.nsplit;
+    DecodeParams& p = r.prm;
+    p.Hq = r.Hq;
+    p.Hkv = r.Hkv;
+    p.G = G;
+    p.chunk = sp.chunk;
+    p.nsplit = sp.nsplit;
+    p.scale_log2 = r.scale * kLog2e;
+    p.part_o = static_cast<float*>(ws);
+    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(rows * r.D * sizeof(float)));
+
+    dim3 grid(sp.nsplit, r.Hkv, r.B);
+    hipError_t e;
+    if (r.fp8) e = launch_split_d<bf16_t, true>(r.D, grid, r.stream, GP, p);
+    else if (r.qdtype == 0) e = launch_split_d<f16_t, false>(r.D, grid, r.stream, GP, p);
+    else e = launch_split_d<bf16_t, false>(r.D, grid, r.stream, GP, p);
+    if (e != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+
+    MergeParams mp;
+    mp.part_o = p.part_o;
+    mp.part_ml = p.part_ml;
+    mp.lens = p.lens;
+    mp.len_plus = p.len_plus;
+    mp.Hq = r.Hq;
+    mp.D = r.D;
+    mp.chunk = sp.chunk;
+    mp.nsplit = sp.nsplit;
+    mp.gate = r.gate;
+    mp.g_bstride = r.g_bstride;
+    mp.g_hstride = r.g_hstride;
+    mp.out = r.out;
+    dim3 mg(r.Hq, r.B, r.D / 64);
+    if (r.qdtype == 0) hipLaunchKernelGGL(decode_merge_kernel<f16_t>, mg, dim3(64), 0, r.stream, mp);
+    else hipLaunchKernelGGL(decode_merge_kernel<bf16_t>, mg, dim3(64), 0, r.stream, mp);
+    if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    return 0;
+}
+
+// Uniform kv_len for the drop-in entry points: a device array of B copies,
+// kept per device and refreshed only when the value or batch changes.
+static const int32_t* uniform_lens(int device, int B, int kv_len, hipStream_t st, size_t ws_need) {
+    (void)ws_need;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    static std::vector<int32_t*> bufs;
+    static std::vector<std::pair<int, int>> keys;
+    if (static_cast<size_t>(device) >= bufs.size()) {
+        bufs.resize(device + 1, nullptr);
+        keys.resize(device + 1, {-1, -1});
+    }
+    if (keys[device].first < B) {
+        if (bufs[device]) (void)hipFree(bufs[device]);
+        bufs[device] = nullptr;
+        int cap = B < 64 ? 64 : B;
+        if (hipMalloc(&bufs[device], cap * sizeof(int32_t)) != hipSuccess) return nullptr;
+        keys[device] = {cap, -1};
+    }
+    if (keys[device].second != kv_len) {
+        std::vector<int32_t> h(keys[device].first, kv_len);
+        if (hipMemcpy(bufs[device], h.data(), h.size() * sizeof(int32_t), hipMemcpyHostToDevice) != hipSuccess)
+            return nullptr;
+        keys[device].second = kv_len;
+    }
+    (void)st;
+    return bufs[device];
+}
+
+static int decode_flat_common(int dtype, size_t device, size_t B, size_t Hq, size_t Hkv, size_t kv_len,
+                              size_t kv_stride, size_t D, size_t groups, float scale, const void* q,
+                              const void* k, const void* v, void* out) {
+    if (dtype != 0 && dtype != 2) return 400;
+    if (D > 256 || (D != 64 && D != 128 && D != 256)) return 401;
+    if (Hkv == 0 || groups == 0 || Hq != Hkv * groups || groups > 16) return 401;
+    ScopedDevice scoped(static_cast<int>(device));
+    const int dev = static_cast<int>(device);
+    const int32_t* lens = uniform_lens(dev, static_cast<int>(B), static_cast<int>(kv_len), nullptr, 0);
+    if (!lens) return 402;
+    DecodeRequest r{};
+    r.qdtype = dtype;
+    r.fp8 = false;
+    r.B = static_cast<int>(B);
+    r.Hq = static_cast<int>(Hq);
+    r.Hkv = static_cast<int>(Hkv);
+    r.D = static_cast<int>(D);
+    r.max_len = static_cast<int>(kv_len);
+    r.scale = scale;
+    r.device = dev;
+    r.stream = nullptr;
+    r.out = out;
+    DecodeParams& p = r.prm;
+    p.kv.k = static_cast<uint8_t*>(const_cast<void*>(k));
+    p.kv.v = static_cast<uint8_t*>(const_cast<void*>(v));
+    p.kv.ks = p.kv.vs = nullptr;
+    p.kv.bt = nullptr;
+    p.kv.page_size = 1;
+    p.kv.head_stride = static_cast<int64_t>(kv_stride) * D;
+    p.kv.seq_stride = static_cast<int64_t>(Hkv) * kv_stride * D;
+    p.q = static_cast<const uint16_t*>(q);
+    p.q_bstride = static_cast<int64_t>(Hq) * D;
+    p.q_hstride = static_cast<int64_t>(D);
+    p.lens = lens;
+    p.len_plus = 0;
+    p.fused = 0;
+    if (kv_len == 0) {
+        // every row is empty: the merge writes zeros
+    }
+    const int rc = run_decode(r);
+    if (rc == SUPERSONIC_ERR_LAUNCH || rc == SUPERSONIC_ERR_WORKSPACE) return 402;
+    if (rc != 0) return 401;
+    if (hipDeviceSynchronize() != hipSuccess) return 403;
+    return 0;
+}
+
+}  // namespace ssa
+
+using namespace ssa;
+
+extern "C" int supersonic_qwen35_hip_full_attention_decode_flat(
+    int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
+    size_t kv_len, size_t head_dim, size_t num_kv_groups, float scale,
+    const void* query, const void* key, const void* value, void* out) {
+    return decode_flat_common(dtype, device_ordinal, batch_size, q_heads, kv_heads, kv_len, kv_len,
+                              head_dim, num_kv_groups, scale, query, key, value, out);
+}
+
+extern "C" int supersonic_qwen35_hip_full_attention_decode_flat_strided(
+    int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
+    size_t kv_len, size_t kv_stride, size_t head_dim, size_t num_kv_groups, float scale,
+    const void* query, const void* key, const void* value, void* out) {
+    if (kv_stride < kv_len) return 401;
+    return decode_flat_common(dtype, device_ordinal, batch_size, q_heads, kv_heads, kv_len, kv_stride,
+                              head_dim, num_kv_groups, scale, query, key, value, out);
+}
+
+extern "C" size_t supersonic_attn_gfx950_decode_workspace_size(
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len) {
+    if (kv_heads == 0) return 0;
+    const SplitPlan sp = plan_splits(static_cast<int>(batch), static_cast<int>(kv_heads),
+                                     max_kv_len ? static_cast<int>(max_kv_len) : 1);
+    return workspace_bytes_for(static_cast<int>(batch), static_cast<int>(q_heads), static_cast<int>(head_dim),
+                               sp.nsplit);
+}
+
+static int check_sizes(size_t a, size_t b, size_t c, size_t d, size_t e) {
+    const size_t lim = 0x7FFFFFFF;
+    return (a > lim || b > lim || c > lim || d > lim || e > lim) ? SUPERSONIC_ERR_RANGE : 0;
+}
+
+extern "C" int supersonic_attn_gfx950_decode(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
+    size_t max_kv_len, float eps, float scale,
+    const void* q_proj, const void* k_new, const void* v_new,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const int32_t* positions, const supersonic_kv_cache* cache, void* out,
+    void* workspace, size_t workspace_bytes) {
+    if (kv_dtype != SUPERSONIC_KV_BF16 && kv_dtype != SUPERSONIC_KV_FP8_E4M3) return SUPERSONIC_ERR_DTYPE;
+    if (int rc = check_sizes(batch, q_heads, kv_heads, head_dim, max_kv_len)) return rc;
+    if (!q_proj || !k_new || !v_new || !q_norm_w || !k_norm_w || !positions || !out) return SUPERSONIC_ERR_NULL;
+    if (rotary_dim % 2 != 0 || rotary_dim > head_dim) return SUPERSONIC_ERR_ROTARY;
+    if (rotary_dim > 0 && (!cos_table || !sin_table)) return SUPERSONIC_ERR_NULL;
+    const bool fp8 = kv_dtype == SUPERSONIC_KV_FP8_E4M3;
+    DecodeRequest r{};
+    if (int rc = make_view(cache, fp8, &r.prm.kv)) return rc;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return SUPERSONIC_ERR_HEAD_DIM;
+    ScopedDevice scoped(static_cast<int>(device_ordinal));
+    r.qdtype = 2;
+    r.fp8 = fp8;
+    r.B = static_cast<int>(batch);
+    r.Hq = static_cast<int>(q_heads);
+    r.Hkv = static_cast<int>(kv_heads);
+    r.D = static_cast<int>(head_dim);
+    r.max_len = static_cast<int>(max_kv_len);
+    r.scale = scale;
+    r.device = static_cast<int>(device_ordinal);
+    r.stream = static_cast<hipStream_t>(stream);
+    r.out = out;
+    r.workspace = workspace;
+    r.workspace_bytes = workspace_bytes;
+    r.gate = static_cast<const uint16_t*>(q_proj) + head_dim;  // per head [q | gate]
+    r.g_bstride = static_cast<int64_t>(q_heads) * 2 * head_dim;
+    r.g_hstride = 2 * static_cast<int64_t>(head_dim);
+    DecodeParams& p = r.prm;
+    p.q = static_cast<const uint16_t*>(q_proj);
+    p.q_bstride = static_cast<int64_t>(q_heads) * 2 * head_dim;
+    p.q_hstride = 2 * static_cast<int64_t>(head_dim);
+    p.lens = positions;
+    p.len_plus = 1;
+    p.fused = 1;
+    p.k_new = static_cast<const uint16_t*>(k_new);
+    p.v_new = static_cast<const uint16_t*>(v_new);
+    p.q_norm_w = static_cast<const uint16_t*>(q_norm_w);
+    p.k_norm_w = static_cast<const uint16_t*>(k_norm_w);
+    p.cos_t = static_cast<const uint16_t*>(cos_table);
+    p.sin_t = static_cast<const uint16_t*>(sin_table);
+    p.half_rot = static_cast<int>(rotary_dim / 2);
+    p.eps = eps;
+    return run_decode(r);
+}
+
+extern "C" int supersonic_attn_gfx950_decode_attend(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len,
+    float scale, const void* q, const int32_t* kv_lens, const supersonic_kv_cache* cache,
+    const void* gate, void* out, void* workspace, size_t workspace_bytes) {
+    if (kv_dtype != SUPERSONIC_KV_BF16 && kv_dtype != SUPERSONIC_KV_FP8_E4M3) return SUPERSONIC_ERR_DTYPE;
+    if (int rc = check_sizes(batch, q_heads, kv_heads, head_dim, max_kv_len)) return rc;
+    if (!q || !kv_lens || !out) return SUPERSONIC_ERR_NULL;
+    const bool fp8 = kv_dtype == SUPERSONIC_KV_FP8_E4M3;
+    DecodeRequest r{};
+    if (int rc = make_view(cache, fp8, &r.prm.kv)) return rc;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return SUPERSONIC_ERR_HEAD_DIM;
+    ScopedDevice scoped(static_cast<int>(device_ordinal));
+    r.qdtype = 2;
+    r.fp8 = fp8;
+    r.B = static_cast<int>(batch);
+    r.Hq = static_cast<int>(q_heads);
+    r.Hkv = static_cast<int>(kv_heads);
+    r.D = static_cast<int>(head_dim);
+    r.max_len = static_cast<int>(max_kv_len);
+    r.scale = scale;
+    r.device = static_cast<int>(device_ordinal);
+    r.stream = static_cast<hipStream_t>(stream);
+    r.out = out;
+    r.workspace = workspace;
+    r.workspace_bytes = workspace_bytes;
+    r.gate = static_cast<const uint16_t*>(gate);
+    r.g_bstride = static_cast<int64_t>(q_heads) * head_dim;
+    r.g_hstride = static_cast<int64_t>(head_dim);
+    DecodeParams& p = r.prm;
+    p.q = static_cast<const uint16_t*>(q);
+    p.q_bstride = static_cast<int64_t>(q_heads) * head_dim;
+    p.q_hstride = static_cast<int64_t>(head_dim);
+    p.lens = kv_lens;
+    p.len_plus = 0;
+    p.fused = 0;
+    return run_decode(r);
+}

@@ -1,0 +1,44 @@
+// Host runtime pieces shared by the bridges: the per-device workspace cache.
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+
+namespace ssa {
+
+namespace {
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::vector<Workspace> g_ws;
+}  // namespace
+
+// Returns a device buffer of at least `bytes` for `device`, growing the cached
+// one when needed.  The buffer is reused by every call on that device, so
+// calls that overlap on one device must pass their own workspace instead.
+void* device_workspace(int device, size_t bytes) {
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if (device < 0) return nullptr;
+    if (static_cast<size_t>(device) >= g_ws.size()) g_ws.resize(device + 1);
+    Workspace& w = g_ws[device];
+    if (w.bytes >= bytes && w.ptr) return w.ptr;
+    if (w.ptr) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.bytes = 0;
+    }
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    if (hipMalloc(&w.ptr, want) != hipSuccess) {
+        w.ptr = nullptr;
+        return nullptr;
+    }
+    w.bytes = want;
+    return w.ptr;
+}
+
+}  // namespace ssa
+
+extern "C" const char* supersonic_attn_version(void) { return "supersonic-attn-gfx950 0.1.0"; }

@@ -1,0 +1,100 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol,
+and the argument-validation paths return the documented status codes without
+touching a GPU (no compute call is made here)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from supersonic_amd import kernel_ffi as K
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = K.header_functions()
+    assert len(names) >= 17
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(K.SIGNATURES)
+
+
+def test_reference_symbols_are_declared():
+    """The drop-in set: every reference bridge symbol on the path
+    (prefill_ffi.rs:635-950) is declared with the reference's name."""
+    need = {
+        "supersonic_qwen35_hip_full_attention_prefill", "supersonic_qwen35_4b_hip_full_attention_prefill",
+        "supersonic_qwen35_hip_full_attention_decode_flat", "supersonic_qwen35_hip_full_attention_decode_flat_strided",
+        "supersonic_qwen35_4b_hip_quantize_kv_to_fp8", "supersonic_qwen35_hip_rms_norm", "supersonic_qwen35_hip_cast",
+        "supersonic_qwen35_hip_apply_rope_prefill", "supersonic_qwen35_hip_transpose_shd_hsd",
+        "supersonic_qwen35_hip_sigmoid_mul", "supersonic_qwen35_hip_split_qgate",
+    }
+    assert need <= set(K.header_functions())
+
+
+def test_kv_cache_struct_layout_matches_header():
+    text = open(os.path.join(ROOT, "include", "supersonic_attn.h")).read()
+    body = re.search(r"typedef struct supersonic_kv_cache \{(.*?)\}", text, re.S).group(1)
+    fields = re.findall(r"(\w+);", body)
+    assert fields == [f[0] for f in K.KvCacheDesc._fields_]
+    assert C.sizeof(K.KvCacheDesc) == 8 * 5 + 8 * 3 + 4 * 2 + 8 * 3
+
+
+def test_version(lib):
+    assert K.version().startswith("supersonic-attn-gfx950")
+
+
+@pytest.mark.parametrize("fn,args,code", [
+    ("supersonic_qwen35_hip_full_attention_prefill", (9, 0, 1, 1, 1, 1, 1, 64, 1, 1.0, 0, None, None, None, None), 64),
+    ("supersonic_qwen35_hip_full_attention_prefill", (2, 0, 1, 1, 1, 1, 1, 96, 1, 1.0, 0, None, None, None, None), 14),
+    ("supersonic_qwen35_hip_full_attention_prefill", (2, 0, 1, 1, 1, 1, 1, 1024, 1, 1.0, 0, None, None, None, None), 14),
+    ("supersonic_qwen35_hip_full_attention_decode_flat", (1, 0, 1, 1, 1, 1, 256, 1, 1.0, None, None, None, None), 400),
+    ("supersonic_qwen35_hip_full_attention_decode_flat", (2, 0, 1, 1, 1, 1, 512, 1, 1.0, None, None, None, None), 401),
+    ("supersonic_qwen35_hip_full_attention_decode_flat_strided",
+     (2, 0, 1, 1, 1, 10, 5, 256, 1, 1.0, None, None, None, None), 401),
+    ("supersonic_qwen35_4b_hip_quantize_kv_to_fp8", (0, 0, None, None, None, 1, 1, 256, 1, 0), 256),
+    ("supersonic_qwen35_hip_rms_norm", (5, 0, 1, 1, 1e-6, 1, None, None, None), 74),
+    ("supersonic_qwen35_hip_cast", (5, 2, 0, 1, None, None), 137),
+    ("supersonic_qwen35_hip_cast", (2, 5, 0, 1, None, None), 137),
+    ("supersonic_qwen35_hip_apply_rope_prefill", (5, 0, 1, 1, 64, 16, None, None, None), 310),
+    ("supersonic_qwen35_hip_transpose_shd_hsd", (5, 0, 1, 1, 1, None, None), 320),
+    ("supersonic_qwen35_hip_sigmoid_mul", (5, 0, 1, None, None, None), 350),
+    ("supersonic_qwen35_hip_split_qgate", (5, 0, 1, 1, 1, None, None, None), 370),
+])
+def test_validation_status_codes(lib, fn, args, code):
+    assert getattr(lib, fn)(*args) == code
+
+
+def test_fused_entry_validation(lib):
+    desc = K.KvCacheDesc()
+    p = 0x1000  # never dereferenced: validation fails first
+    dec = lambda kvd, hd, rot, q=p: lib.supersonic_attn_gfx950_decode(
+        0, None, kvd, 1, 8, 2, hd, rot, 16, 1e-6, 0.0625, q, p, p, p, p, p, p, p, C.byref(desc), p, None, 0)
+    assert dec(7, 256, 64) == K.ERR["DTYPE"]
+    assert dec(2, 256, 64, q=None) == K.ERR["NULL"]
+    assert dec(2, 256, 63) == K.ERR["ROTARY"]
+    assert dec(2, 256, 64) == K.ERR["NULL"]          # the cache view has no K pointer
+    desc.k = desc.v = p
+    assert dec(3, 256, 64) == K.ERR["NULL"]          # fp8 without scale pointers
+    assert dec(2, 96, 32) == K.ERR["HEAD_DIM"]
+    desc.block_table = p
+    desc.page_size = 40
+    desc.max_pages_per_seq = 4
+    assert dec(2, 256, 64) == K.ERR["CACHE"]         # pages must hold whole 16-token blocks
+    desc.block_table = None
+    pre = lambda kvd, hq, hkv, hd, rot: lib.supersonic_attn_gfx950_prefill(
+        0, None, kvd, hq, hkv, hd, rot, 16, 0, 1e-6, 0.0625, p, p, p, p, p, p, p, C.byref(desc), p)
+    assert pre(9, 16, 4, 256, 64) == K.ERR["DTYPE"]
+    assert pre(2, 16, 5, 256, 64) == K.ERR["HEADS"]
+    assert pre(2, 16, 4, 200, 64) == K.ERR["HEAD_DIM"]
+    assert pre(2, 16, 4, 256, 40) == K.ERR["ROTARY"]
+    att = lambda kvd: lib.supersonic_attn_gfx950_decode_attend(0, None, kvd, 1, 8, 2, 256, 16, 0.0625, None, p,
+                                                               C.byref(desc), None, p, None, 0)
+    assert att(2) == K.ERR["NULL"]
+
+
+def test_workspace_size_is_host_only(lib):
+    n = K.decode_workspace_size(1, 16, 4, 256, 32769)
+    assert n > 16 * 256 * 4
+    assert K.decode_workspace_size(8, 16, 4, 256, 32769) >= n

@@ -1,0 +1,220 @@
+"""GPU parity of the decode path through the C ABI (split-K kernels).
+
+Every case compares the HIP result with the CPU oracle on identical seeded
+inputs: BF16 KV within max-abs 2e-2 / mean-abs 2e-3, FP8 KV within the looser
+bound stated in gpu_util.TOL_FP8, appended cache bytes bit-exact.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, TOL_BF16, TOL_FP8, announce, check, dev, gen, make_decode_case, oracle_decode
+from oracle import attn_oracle as O
+from supersonic_amd import kernel_ffi as K
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def run_fused(case, paged=None, workspace=None):
+    B = case["q_proj"].shape[0]
+    sh = case["shape"]
+    if paged is None:
+        cache = K.KvCache(dev(case["k"]), dev(case["v"]), dev(case["ks"]), dev(case["vs"]))
+    else:
+        cache = paged
+    out = torch.zeros(B, sh.q_heads * sh.head_dim, dtype=torch.bfloat16, device=DEV)
+    K.fused_decode(0, dev(case["q_proj"]), dev(case["k_new"]), dev(case["v_new"]), dev(case["qw"]),
+                   dev(case["kw"]), dev(case["cos"]), dev(case["sin"]), dev(case["pos"]), cache, out,
+                   q_heads=sh.q_heads, kv_heads=sh.kv_heads, head_dim=sh.head_dim, rotary_dim=sh.rotary_dim,
+                   max_kv_len=int(case["pos"].max()) + 1, workspace=workspace)
+    torch.cuda.synchronize()
+    return out, cache
+
+
+# ----------------------------------------------------------- drop-in decode_flat
+def test_decode_flat_golden_via_attend():
+    announce("decode_attend golden decode_tiny")
+    g = json.load(open(os.path.join(GOLD, "decode_tiny.json")))
+    B, Hq, Hkv, T, D = g["B"], g["Hq"], g["Hkv"], g["T"], g["D"]
+    q = torch.tensor(g["q"]).reshape(B, Hq, D).bfloat16().to(DEV)
+    k = torch.tensor(g["k"]).reshape(B, Hkv, T, D).bfloat16().to(DEV)
+    v = torch.tensor(g["v"]).reshape(B, Hkv, T, D).bfloat16().to(DEV)
+    lens = torch.tensor(g["lens"], dtype=torch.int32, device=DEV)
+    out = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    K.decode_attend(0, q, lens, K.KvCache(k, v), out, q_heads=Hq, kv_heads=Hkv, head_dim=D, max_kv_len=T)
+    torch.cuda.synchronize()
+    ref = torch.tensor(g["out"]).reshape(B, Hq * D)
+    check(out, ref, (2 ** -7, 1e-3), "decode_tiny")
+
+
+@pytest.mark.parametrize("dtype", [K.ScalarType.BF16, K.ScalarType.F16])
+@pytest.mark.parametrize("B,Hq,Hkv,D,L", [(1, 8, 2, 256, 2048), (3, 16, 4, 128, 777), (2, 4, 4, 64, 1),
+                                         (1, 16, 1, 256, 4099)])
+def test_decode_flat_matches_oracle(dtype, B, Hq, Hkv, D, L):
+    announce(f"decode_flat dtype={dtype} B={B} Hq={Hq} Hkv={Hkv} D={D} L={L}")
+    tdt = torch.bfloat16 if dtype == K.ScalarType.BF16 else torch.float16
+    g = gen(11)
+    q = torch.randn(B, Hq, D, generator=g).to(tdt)
+    k = torch.randn(B, Hkv, L, D, generator=g).to(tdt)
+    v = torch.randn(B, Hkv, L, D, generator=g).to(tdt)
+    out = torch.zeros(B, Hq * D, dtype=tdt, device=DEV)
+    K.full_attention_decode_flat(0, dtype, B, Hq, Hkv, L, D, D ** -0.5, q.to(DEV), k.to(DEV), v.to(DEV), out)
+    ref = O.attention_decode(q.float(), k.float(), v.float(), L, D ** -0.5).reshape(B, Hq * D)
+    check(out, ref, TOL_BF16, "decode_flat")
+
+
+def test_decode_flat_strided_cache():
+    announce("decode_flat_strided")
+    B, Hq, Hkv, D, L, cap = 2, 8, 2, 256, 1000, 1280
+    g = gen(12)
+    q = O.randn_bf16(g, B, Hq, D)
+    k = O.randn_bf16(g, B, Hkv, cap, D)
+    v = O.randn_bf16(g, B, Hkv, cap, D)
+    out = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    K.full_attention_decode_flat_strided(0, K.ScalarType.BF16, B, Hq, Hkv, L, cap, D, D ** -0.5, q.to(DEV),
+                                         k.to(DEV), v.to(DEV), out)
+    ref = O.attention_decode(q, k, v, L, D ** -0.5).reshape(B, Hq * D)
+    check(out, ref, TOL_BF16, "strided")
+
+
+def test_decode_flat_error_codes():
+    g = torch.zeros(16, device=DEV)
+    lib = K.load()
+    assert lib.supersonic_qwen35_hip_full_attention_decode_flat(1, 0, 1, 1, 1, 1, 256, 1, 1.0, g.data_ptr(),
+                                                                g.data_ptr(), g.data_ptr(), g.data_ptr()) == 400
+    assert lib.supersonic_qwen35_hip_full_attention_decode_flat(2, 0, 1, 1, 1, 1, 512, 1, 1.0, g.data_ptr(),
+                                                                g.data_ptr(), g.data_ptr(), g.data_ptr()) == 401
+
+
+def test_decode_split_invariance(monkeypatch):
+    """The split-K result does not depend on the chunk size (LSE merge identity)."""
+    announce("decode split invariance")
+    B, Hq, Hkv, D, L = 1, 16, 4, 256, 8192
+    g = gen(13)
+    q = O.randn_bf16(g, B, Hq, D).to(DEV)
+    k = O.randn_bf16(g, B, Hkv, L, D).to(DEV)
+    v = O.randn_bf16(g, B, Hkv, L, D).to(DEV)
+    outs = []
+    for chunk in ("64", "256", "4096"):
+        monkeypatch.setenv("SUPERSONIC_DECODE_MIN_CHUNK", chunk)
+        out = torch.zeros(B, Hq * D, dtype=torch.float16, device=DEV)
+        o32 = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+        K.full_attention_decode_flat(0, K.ScalarType.BF16, B, Hq, Hkv, L, D, D ** -0.5, q, k, v, o32)
+        outs.append(o32.float().cpu())
+    for o in outs[1:]:
+        assert (o - outs[0]).abs().max().item() <= 2 ** -8
+
+
+# ----------------------------------------------------------- fused decode
+def test_fused_decode_golden():
+    announce("fused decode golden")
+    g = json.load(open(os.path.join(GOLD, "fused_decode_tiny.json")))
+    D, Hq, Hkv, pos, rot = g["D"], g["Hq"], g["Hkv"], g["pos"], g["rotary_dim"]
+    cap = pos + 9
+    k = torch.zeros(1, Hkv, cap, D, dtype=torch.bfloat16)
+    v = torch.zeros(1, Hkv, cap, D, dtype=torch.bfloat16)
+    k[0, :, :pos] = torch.tensor(g["cache_k"]).reshape(Hkv, pos, D).bfloat16()
+    v[0, :, :pos] = torch.tensor(g["cache_v"]).reshape(Hkv, pos, D).bfloat16()
+    cos, sin = O.rope_tables(rot, cap, g["theta"])
+    case = dict(q_proj=torch.tensor(g["q_proj"]).reshape(1, -1).bfloat16(),
+                k_new=torch.tensor(g["k_raw"]).reshape(1, -1).bfloat16(),
+                v_new=torch.tensor(g["v_raw"]).reshape(1, -1).bfloat16(),
+                qw=torch.tensor(g["q_norm_w"]).bfloat16(), kw=torch.tensor(g["k_norm_w"]).bfloat16(),
+                cos=cos, sin=sin, pos=torch.tensor([pos], dtype=torch.int32), k=k, v=v, ks=None, vs=None,
+                shape=O.LayerShape(Hq, Hkv, D, rot, g["eps"]))
+    out, cache = run_fused(case)
+    check(out, torch.tensor(g["out"]).reshape(1, -1), (2 ** -7, 1e-3), "fused golden")
+    kg = cache.k[0, :, pos].float().cpu().reshape(-1)
+    kexp = torch.tensor(g["k_rot_expected"])
+    assert (kg - kexp).abs().max().item() <= 2 ** -7 * kexp.abs().max().item()
+    assert torch.equal(cache.v[0, :, pos].cpu(), case["v_new"].reshape(Hkv, D))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,rot,lens", [
+    (1, 8, 2, 256, 64, [2048]),                 # config 1
+    (2, 16, 4, 256, 64, [300, 15]),
+    (3, 8, 1, 128, 32, [1, 64, 129]),
+    (1, 4, 2, 64, 16, [0]),                      # first token: attention over itself
+])
+def test_fused_decode_bf16(B, Hq, Hkv, D, rot, lens):
+    announce(f"fused decode bf16 B={B} Hq={Hq} Hkv={Hkv} D={D} lens={lens}")
+    case = make_decode_case(21, B, Hq, Hkv, D, rot, lens)
+    out, cache = run_fused(case)
+    ref, k_ref, v_ref, _, _ = oracle_decode(case)
+    check(out, ref, TOL_BF16, "fused bf16")
+    for b, p in enumerate(lens):
+        kd = (cache.k[b, :, p].float().cpu() - k_ref[b, :, p].float()).abs()
+        assert kd.max().item() <= 2 ** -7 * k_ref[b, :, p].float().abs().max().item()
+        assert torch.equal(cache.v[b, :, p].cpu(), v_ref[b, :, p])
+        # the rest of the cache is untouched
+        assert torch.equal(cache.k[b, :, :p].cpu(), case["k"][b, :, :p])
+
+
+@pytest.mark.parametrize("B,lens", [(4, [1024, 16383, 5000, 77]), (2, [0, 33])])
+def test_fused_decode_fp8(B, lens):
+    announce(f"fused decode fp8 lens={lens}")
+    case = make_decode_case(31, B, 16, 4, 256, 64, lens, fp8=True)
+    out, cache = run_fused(case)
+    ref, k_ref, v_ref, ks_ref, vs_ref = oracle_decode(case, codec="ocp")
+    check(out, ref, TOL_FP8, "fused fp8")
+    for b, p in enumerate(lens):
+        kc = cache.k[b, :, p].cpu()
+        # codes of the appended row: identical unless the normalised k differs by a bf16 ulp
+        assert (kc != k_ref[b, :, p]).float().mean().item() < 0.02
+        assert torch.equal(cache.v[b, :, p].cpu(), v_ref[b, :, p])
+        assert torch.allclose(cache.v_scale[b, :, p].cpu(), vs_ref[b, :, p])
+
+
+def test_fused_decode_paged():
+    """Config-5 style: block-paged cache of 64-token pages, G = 8, ragged lengths."""
+    B, Hq, Hkv, D, rot, ps = 5, 16, 2, 256, 64, 64
+    lens = [511, 64, 2000, 0, 1337]
+    announce(f"fused decode paged lens={lens}")
+    case = make_decode_case(41, B, Hq, Hkv, D, rot, lens, cap=2048)
+    pages_per = 2048 // ps
+    perm = torch.randperm(B * pages_per, generator=gen(5))
+    kp = torch.zeros(B * pages_per, Hkv, ps, D, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    bt = torch.zeros(B, pages_per, dtype=torch.int32)
+    for b in range(B):
+        for j in range(pages_per):
+            pg = int(perm[b * pages_per + j])
+            bt[b, j] = pg
+            kp[pg] = case["k"][b, :, j * ps:(j + 1) * ps]
+            vp[pg] = case["v"][b, :, j * ps:(j + 1) * ps]
+    cache = K.KvCache(kp.to(DEV), vp.to(DEV), block_table=bt.to(DEV))
+    out, cache = run_fused(case, paged=cache)
+    ref, k_ref, v_ref, _, _ = oracle_decode(case)
+    check(out, ref, TOL_BF16, "paged")
+    for b, p in enumerate(lens):
+        pg = int(bt[b, p // ps])
+        assert torch.equal(cache.v[pg, :, p % ps].cpu(), v_ref[b, :, p])
+
+
+def test_fused_decode_config2_full_size():
+    """Config 2: Qwen3.5-9B shape, 32k context, batch 8."""
+    announce("fused decode config 2, B=8, L=32768")
+    B = 8
+    case = make_decode_case(51, B, 16, 4, 256, 64, [32768] * B)
+    out, _ = run_fused(case)
+    ref, *_ = oracle_decode(case)
+    check(out, ref, TOL_BF16, "config2")
+
+
+def test_fused_decode_errors():
+    lib = K.load()
+    z = torch.zeros(64, device=DEV)
+    desc = K.KvCacheDesc()
+    p = z.data_ptr()
+    args = lambda kvd, hd, rot: (0, None, kvd, 1, 8, 2, hd, rot, 16, 1e-6, 0.0625, p, p, p, p, p, p, p, p,
+                                 K.C.byref(desc), p, None, 0)
+    assert lib.supersonic_attn_gfx950_decode(*args(7, 256, 64)) == K.ERR["DTYPE"]
+    assert lib.supersonic_attn_gfx950_decode(*args(2, 256, 64)) == K.ERR["NULL"]  # cache k is NULL
+    desc.k = desc.v = p
+    assert lib.supersonic_attn_gfx950_decode(*args(2, 96, 32)) == K.ERR["HEAD_DIM"]
+    assert lib.supersonic_attn_gfx950_decode(*args(2, 256, 63)) == K.ERR["ROTARY"]
