@@ -1,0 +1,339 @@
+"""Benchmark of the gfx950 full-attention hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extra]
+
+Headline (``value``): BASELINE config 2, the Qwen3.5-9B decode attention at
+32k context, batch 8: one *step* is one ``supersonic_attn_gfx950_decode`` call
+(QK RMSNorm + partial RoPE + KV append + split-K attention + LSE merge +
+sigmoid gate) for all 8 sequences.  ``value`` is algorithmic bytes per step
+(K+V of 32768 cached tokens per sequence, plus q, gate and out
+section 2) / measured time per step, in GB/s.  Inputs are synthetic N(0,1)
+tensors resident in HBM before the timed region; the KV caches (1.07 GB) are
+larger than the 256 MB last-level cache, so every step streams HBM.
+
+``roofline`` is for the dominant kernel (``decode_split_kernel``), timed live
+with HIP events recorded on its launch stream around each launch.
+``cpu_baseline`` is the repo's torch fp32 oracle timed on this host for the
+same workload.  ``extra`` holds the other BASELINE configs (decode B=1,
+causal prefill at 4096 tokens, FP8-KV ragged decode, mixed paged batch).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-extra", action="store_true")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode1|prefill|fp8|mixed|copy")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", args.gpus))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the attention hot path is "
+                                   "single-GPU (how it would shard is described in DESIGN.md); "
+                                   f"got --gpus {args.gpus}"}))
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from supersonic_amd import kernel_ffi as K
+    K.load()
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    W = Workloads(torch, K, dev, args.steps, args.warmup)
+    if args.only:
+        r = getattr(W, args.only)()
+        print(json.dumps(r, indent=None))
+        return
+
+    head = W.decode8()
+    out = {
+        "metric": "decode attn GB/s (% of 8 TB/s HBM); prefill attn TFLOPS (% MFMA peak)",
+        "value": round(head["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 2: Qwen3.5-9B decode attention, fused QK-norm/RoPE/KV-append/"
+                        "split-K/gate, bf16 KV cache",
+            "batch": 8, "q_heads": 16, "kv_heads": 4, "head_dim": 256, "rotary_dim": 64,
+            "kv_len": 32768, "bytes_per_step": head["bytes"],
+        },
+        "roofline": head["roofline"],
+    }
+    if not args.skip_cpu:
+        out["cpu_baseline"] = W.cpu_decode8()
+    if not args.skip_extra:
+        out["extra"] = {k: getattr(W, k)() for k in ("decode1", "prefill", "fp8", "mixed")}
+    print(json.dumps(out))
+
+
+class Workloads:
+    def __init__(self, torch, K, dev, steps, warmup):
+        self.torch, self.K, self.dev = torch, K, dev
+        self.steps, self.warmup = steps, warmup
+        from oracle import attn_oracle  # only for rope tables of the synthetic inputs
+        self.O = attn_oracle
+
+    # ------------------------------------------------------------ helpers
+    def randn(self, *shape, dtype=None, seed=0):
+        torch = self.torch
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        return torch.randn(*shape, generator=g, device=self.dev, dtype=torch.float32).to(dtype or torch.bfloat16)
+
+    def events(self, n):
+        torch = self.torch
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        for e in evs:
+            e.record()  # creates the underlying hipEvent_t
+        torch.cuda.synchronize()
+        return evs
+
+    def timed(self, step, n_copies=1):
+        """Run warmup + steps of `step(i, before, after)`; returns whole-step ms and
+        the dominant kernel's mean ms (events armed around it)."""
+        torch, K = self.torch, self.K
+        for i in range(self.warmup):
+            step(i % n_copies)
+        torch.cuda.synchronize()
+        kb = self.events(self.steps)
+        ka = self.events(self.steps)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        for i in range(self.steps):
+            K.set_profile_events(kb[i], ka[i])
+            step(i % n_copies)
+        t1.record()
+        torch.cuda.synchronize()
+        K.set_profile_events(None, None)
+        step_ms = t0.elapsed_time(t1) / self.steps
+        kern = [kb[i].elapsed_time(ka[i]) for i in range(self.steps)]
+        return step_ms, statistics.mean(kern), kern
+
+    @staticmethod
+    def decode_bytes(lens, Hq, Hkv, D, kv_esz, scale_bytes=0):
+        kv = sum(lens) * Hkv * (D * kv_esz + scale_bytes) * 2
+        qgo = len(lens) * (Hq * 2 * D * 2 + Hq * D * 2)
+        return kv, kv + qgo
+
+    def make_decode(self, B, lens, Hq, Hkv, D, rot, fp8=False, cap=None, seed=1, paged_ps=None):
+        torch, K = self.torch, self.K
+        cap = cap or (max(lens) + 1)
+        q_proj = self.randn(B, Hq * 2 * D, seed=seed)
+        k_new = self.randn(B, Hkv * D, seed=seed + 1)
+        v_new = self.randn(B, Hkv * D, seed=seed + 2)
+        qw = (self.randn(D, seed=seed + 3).float() * 0.02 + 1).bfloat16()
+        kw = (self.randn(D, seed=seed + 4).float() * 0.02 + 1).bfloat16()
+        cos, sin = self.O.rope_tables(rot, cap + 1, 1.0e7)
+        pos = torch.tensor(lens, dtype=torch.int32, device=self.dev)
+        per_cache = B * Hkv * cap * D * (1 if fp8 else 2) * 2
+        n_copies = max(1, min(8, math.ceil(2 * MALL_BYTES / per_cache)))
+        caches = []
+        for c in range(n_copies):
+            if paged_ps:
+                pages_per = cap // paged_ps
+                shape = (B * pages_per, Hkv, paged_ps, D)
+                bt = torch.randperm(B * pages_per, device=self.dev).to(torch.int32).reshape(B, pages_per)
+            else:
+                shape = (B, Hkv, cap, D)
+                bt = None
+            kk = self.randn(*shape, seed=100 + 2 * c)
+            vv = self.randn(*shape, seed=101 + 2 * c)
+            if fp8:
+                ks = (kk.float().abs().amax(-1) / 448).clamp(min=1e-12)
+                vs = (vv.float().abs().amax(-1) / 448).clamp(min=1e-12)
+                kq = (kk.float() / ks[..., None]).to(torch.float8_e4m3fn).view(torch.uint8)
+                vq = (vv.float() / vs[..., None]).to(torch.float8_e4m3fn).view(torch.uint8)
+                del kk, vv
+                caches.append(K.KvCache(kq, vq, ks.contiguous(), vs.contiguous(), bt))
+            else:
+                caches.append(K.KvCache(kk, vv, block_table=bt))
+        out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=self.dev)
+        ws = torch.empty(K.decode_workspace_size(B, Hq, Hkv, D, max(lens) + 1), dtype=torch.uint8, device=self.dev)
+        args = dict(q_proj=q_proj, k_new=k_new, v_new=v_new, qw=qw, kw=kw, cos=cos.to(self.dev),
+                    sin=sin.to(self.dev), pos=pos, out=out, ws=ws)
+
+        def step(i):
+            K.fused_decode(0, args["q_proj"], args["k_new"], args["v_new"], args["qw"], args["kw"], args["cos"],
+                           args["sin"], args["pos"], caches[i], args["out"], q_heads=Hq, kv_heads=Hkv,
+                           head_dim=D, rotary_dim=rot, max_kv_len=max(lens) + 1, workspace=args["ws"])
+        return step, n_copies
+
+    def decode_result(self, name, B, lens, Hq, Hkv, D, rot, fp8=False, paged_ps=None, cap=None):
+        step, n = self.make_decode(B, lens, Hq, Hkv, D, rot, fp8=fp8, paged_ps=paged_ps, cap=cap)
+        step_ms, kern_ms, _ = self.timed(step, n)
+        kv_bytes, bytes_step = self.decode_bytes(lens, Hq, Hkv, D, 1 if fp8 else 2, 4 if fp8 else 0)
+        # dominant kernel's algorithmic bytes: K+V (+scales) and q
+        kern_bytes = kv_bytes + B * Hq * D * 2
+        ach = kern_bytes / (kern_ms * 1e-3) / 1e9
+        self.torch.cuda.empty_cache()
+        return {
+            "workload": name, "gbs": bytes_step / (step_ms * 1e-3) / 1e9, "ms_per_step": step_ms,
+            "bytes": bytes_step, "kernel_ms": kern_ms, "cache_copies": n,
+            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "decode_split_kernel", "bytes_per_launch": kern_bytes},
+        }
+
+    # ------------------------------------------------------------ workloads
+    def decode8(self):
+        return self.decode_result("config 2, B=8, L=32768", 8, [32768] * 8, 16, 4, 256, 64)
+
+    def decode1(self):
+        r = self.decode_result("config 2, B=1, L=32768", 1, [32768], 16, 4, 256, 64)
+        r["gbs"] = round(r["gbs"], 2)
+        return r
+
+    def fp8(self):
+        torch = self.torch
+        g = torch.Generator().manual_seed(4)
+        lens = torch.randint(1024, 16385, (16,), generator=g).tolist()
+        r = self.decode_result("config 4, FP8 e4m3 KV, B=16, L~U[1024,16384]", 16, lens, 16, 4, 256, 64,
+                               fp8=True, cap=16385)
+        r["lens_sum"] = sum(lens)
+        return r
+
+    def prefill_case(self, S, Hq, Hkv, D, rot, start=0, seed=7, paged_ps=None):
+        torch, K = self.torch, self.K
+        q_proj = self.randn(S, Hq * 2 * D, seed=seed)
+        k_new = self.randn(S, Hkv * D, seed=seed + 1)
+        v_new = self.randn(S, Hkv * D, seed=seed + 2)
+        qw = (self.randn(D, seed=seed + 3).float() * 0.02 + 1).bfloat16()
+        kw = (self.randn(D, seed=seed + 4).float() * 0.02 + 1).bfloat16()
+        cos, sin = self.O.rope_tables(rot, start + S + 1, 1.0e7)
+        cos, sin = cos.to(self.dev), sin.to(self.dev)
+        L = start + S
+        if paged_ps:
+            npg = (L + paged_ps - 1) // paged_ps
+            cache = K.KvCache(torch.zeros(npg, Hkv, paged_ps, D, dtype=torch.bfloat16, device=self.dev),
+                              torch.zeros(npg, Hkv, paged_ps, D, dtype=torch.bfloat16, device=self.dev),
+                              block_table=torch.randperm(npg, device=self.dev).to(torch.int32).reshape(1, -1))
+        else:
+            cache = K.KvCache(torch.zeros(1, Hkv, L, D, dtype=torch.bfloat16, device=self.dev),
+                              torch.zeros(1, Hkv, L, D, dtype=torch.bfloat16, device=self.dev))
+        out = torch.empty(S, Hq * D, dtype=torch.bfloat16, device=self.dev)
+
+        def step(i):
+            K.fused_prefill(0, q_proj, k_new, v_new, qw, kw, cos, sin, cache, out, q_heads=Hq, kv_heads=Hkv,
+                            head_dim=D, rotary_dim=rot, chunk_start=start)
+        return step
+
+    @staticmethod
+    def causal_flops(S, Hq, D, start=0):
+        # QK^T + PV over the causal lower triangle including the diagonal
+        keys = sum(min(start + p + 1, start + S) for p in range(S)) if start else S * (S + 1) // 2
+        return 4 * Hq * D * keys
+
+    def prefill(self):
+        S, Hq, Hkv, D, rot = 4096, 16, 4, 256, 64
+        step = self.prefill_case(S, Hq, Hkv, D, rot)
+        step_ms, kern_ms, _ = self.timed(step)
+        fl = self.causal_flops(S, Hq, D)
+        ach = fl / (kern_ms * 1e-3) / 1e12
+        return {"workload": "config 3, causal prefill S=4096, 16/4 heads, D=256, fused norm/RoPE/gate",
+                "tflops_step": fl / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms, "kernel_ms": kern_ms,
+                "flops": fl,
+                "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                             "kernel": "prefill_kernel"}}
+
+    def mixed(self):
+        """Config 5: one 8192-token prefill chunk + 32 decode sequences, 16/2 heads,
+        paged KV with 64-token pages; the two calls run back to back on one stream."""
+        torch = self.torch
+        Hq, Hkv, D, rot = 16, 2, 256, 64
+        g = torch.Generator().manual_seed(5)
+        lens = torch.randint(512, 65537, (32,), generator=g).tolist()
+        pstep = self.prefill_case(8192, Hq, Hkv, D, rot, seed=9, paged_ps=64)
+        p_ms, p_kern, _ = self.timed(pstep)
+        dstep, n = self.make_decode(32, lens, Hq, Hkv, D, rot, paged_ps=64, cap=65600, seed=11)
+        d_ms, d_kern, _ = self.timed(dstep, n)
+
+        def both(i):
+            pstep(i)
+            dstep(i % n)
+        tot_ms, _, _ = self.timed(both, n)
+        fl = self.causal_flops(8192, Hq, D)
+        kv_bytes, d_bytes = self.decode_bytes(lens, Hq, Hkv, D, 2)
+        self.torch.cuda.empty_cache()
+        return {"workload": "config 5, 8192-token chunk + 32 paged decode seqs (16/2 heads, pages of 64)",
+                "ms_per_step": tot_ms, "prefill_kernel_ms": p_kern, "decode_kernel_ms": d_kern,
+                "prefill_tflops": fl / (p_kern * 1e-3) / 1e12,
+                "prefill_frac": fl / (p_kern * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                "decode_gbs": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9,
+                "decode_frac": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "lens_sum": sum(lens)}
+
+    def copy(self):
+        """Plain device copy of known size, to calibrate FETCH_SIZE/WRITE_SIZE counters."""
+        torch = self.torch
+        n = 512 << 20
+        a = torch.empty(n, dtype=torch.uint8, device=self.dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        return {"workload": "copy", "bytes": n}
+
+    def cpu_decode8(self):
+        """The torch fp32 oracle on this host's cores: one config-2 B=8 step."""
+        import torch
+        O = self.O
+        torch.set_num_threads(min(16, os.cpu_count() or 1))
+        g = torch.Generator().manual_seed(3)
+        B, Hq, Hkv, D, rot, L = 8, 16, 4, 256, 64, 32768
+        shape = O.LayerShape(Hq, Hkv, D, rot)
+        q_proj = O.randn_bf16(g, B, Hq * 2 * D)
+        k_new = O.randn_bf16(g, B, Hkv * D)
+        v_new = O.randn_bf16(g, B, Hkv * D)
+        qw, kw = O.norm_weights(g, D)
+        cos, sin = O.rope_tables(rot, L + 1, 1.0e7)
+        kc = [O.randn_bf16(g, Hkv, L + 1, D) for _ in range(B)]
+        vc = [O.randn_bf16(g, Hkv, L + 1, D) for _ in range(B)]
+        pos = [L] * B
+        O.decode_layer(shape, q_proj, k_new, v_new, qw, kw, cos, sin, pos, kc, vc)  # warm-up
+        times = []
+        t_end = time.perf_counter() + 30.0
+        while len(times) < 5 and (len(times) < 2 or time.perf_counter() < t_end):
+            t = time.perf_counter()
+            O.decode_layer(shape, q_proj, k_new, v_new, qw, kw, cos, sin, pos, kc, vc)
+            times.append(time.perf_counter() - t)
+        med = statistics.median(times)
+        _, bytes_step = self.decode_bytes([L] * B, Hq, Hkv, D, 2)
+        return {"value": round(bytes_step / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port", "seconds_per_step": round(med, 4),
+                "sample": f"oracle.attn_oracle.decode_layer (torch fp32) on one full config-2 B=8 step, "
+                          f"median of {len(times)} runs after 1 warm-up"}
+
+
+if __name__ == "__main__":
+    main()

@@ -217,6 +217,12 @@ int supersonic_attn_gfx950_quantize_kv_fp8_ocp(
     size_t device_ordinal, void* stream, const void* src, void* dst_fp8, float* dst_scale,
     int num_kv_heads, int seq_len, int head_dim, int max_T, int pos_offset);
 
+/* Benchmark hook (no reference counterpart): two hipEvent_t recorded on the
+ * launch stream right before and right after the dominant kernel (split-K
+ * decode kernel, MFMA prefill kernel) of the next fused-entry call on any
+ * thread; the pair is consumed by that call.  NULL, NULL clears it. */
+void supersonic_attn_gfx950_set_profile_events(void* before, void* after);
+
 /* Library version string. */
 const char* supersonic_attn_version(void);
 

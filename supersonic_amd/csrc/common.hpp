@@ -176,6 +176,15 @@ struct ScopedDevice {
 // that have no workspace argument.
 void* device_workspace(int device, size_t bytes);
 
+// Optional pair of events recorded on the launch stream immediately before and
+// after the dominant kernel of the next entry-point call (benchmarks time that
+// kernel on its own stream with them).  Cleared after use.
+struct ProfileEvents {
+    hipEvent_t before = nullptr;
+    hipEvent_t after = nullptr;
+};
+ProfileEvents take_profile_events();
+
 inline unsigned grid1d(size_t n, int block) {
     return static_cast<unsigned>((n + block - 1) / block);
 }

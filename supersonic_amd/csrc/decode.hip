@@ -599,11 +599,14 @@ static int run_decode(DecodeRequest& r) {
     p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(rows * r.D * sizeof(float)));
 
     dim3 grid(sp.nsplit, r.Hkv, r.B);
+    const ProfileEvents prof = take_profile_events();
+    if (prof.before) (void)hipEventRecord(prof.before, r.stream);
     hipError_t e;
     if (r.fp8) e = launch_split_d<bf16_t, true>(r.D, grid, r.stream, GP, p);
     else if (r.qdtype == 0) e = launch_split_d<f16_t, false>(r.D, grid, r.stream, GP, p);
     else e = launch_split_d<bf16_t, false>(r.D, grid, r.stream, GP, p);
     if (e != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    if (prof.after) (void)hipEventRecord(prof.after, r.stream);
 
     MergeParams mp;
     mp.part_o = p.part_o;

@@ -611,7 +611,10 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.half_rot = static_cast<int>(rotary_dim / 2);
     p.eps = eps;
     dim3 grid(p.nqt, static_cast<unsigned>(q_heads), 1);
+    const ProfileEvents prof = take_profile_events();
+    if (prof.before) (void)hipEventRecord(prof.before, st);
     if (launch_prefill<bf16_t, true>(static_cast<int>(head_dim), grid, st, p) != hipSuccess)
         return SUPERSONIC_ERR_LAUNCH;
+    if (prof.after) (void)hipEventRecord(prof.after, st);
     return 0;
 }

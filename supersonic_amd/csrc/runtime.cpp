@@ -39,6 +39,24 @@ void* device_workspace(int device, size_t bytes) {
     return w.ptr;
 }
 
+namespace {
+std::mutex g_prof_mutex;
+ProfileEvents g_prof;
+}  // namespace
+
+ProfileEvents take_profile_events() {
+    std::lock_guard<std::mutex> lock(g_prof_mutex);
+    ProfileEvents e = g_prof;
+    g_prof = ProfileEvents{};
+    return e;
+}
+
 }  // namespace ssa
+
+extern "C" void supersonic_attn_gfx950_set_profile_events(void* before, void* after) {
+    std::lock_guard<std::mutex> lock(ssa::g_prof_mutex);
+    ssa::g_prof.before = static_cast<hipEvent_t>(before);
+    ssa::g_prof.after = static_cast<hipEvent_t>(after);
+}
 
 extern "C" const char* supersonic_attn_version(void) { return "supersonic-attn-gfx950 0.1.0"; }

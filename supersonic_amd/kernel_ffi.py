@@ -91,9 +91,11 @@ SIGNATURES = {
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
          _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
+    "supersonic_attn_gfx950_set_profile_events": [_p, _p],
     "supersonic_attn_version": [],
 }
-RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_version": C.c_char_p}
+RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
+            "supersonic_attn_gfx950_set_profile_events": None}
 
 _LIB = None
 
@@ -314,6 +316,12 @@ def quantize_kv_fp8_ocp(ordinal, src, dst_fp8, dst_scale, num_kv_heads, seq_len,
         ordinal, _stream_ptr(stream), _ptr(src), _ptr(dst_fp8), _ptr(dst_scale), num_kv_heads, seq_len,
         head_dim, max_t, pos_offset)
     _check("quantize_kv_fp8_ocp", st)
+
+
+def set_profile_events(before, after):
+    """Arm the benchmark hook with two torch.cuda.Event (enable_timing=True)."""
+    load().supersonic_attn_gfx950_set_profile_events(None if before is None else before.cuda_event,
+                                                     None if after is None else after.cuda_event)
 
 
 def version() -> str:
