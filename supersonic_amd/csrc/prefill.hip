@@ -48,6 +48,7 @@ struct PrefillParams {
     const uint16_t* sin_t;
     int half_rot;
     float eps;
+    float rescale_slack;  // lazy-rescale slack in log2 units (0 = exact running max)
 };
 
 template <typename QT> struct Mfma32;
@@ -76,28 +77,81 @@ __device__ __forceinline__ uint32_t pk2(float a, float b) {
     return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);
 }
 
-// Position of key w (0..15) inside its 16-key group of the V^T tile: keys
-// {0-3, 8-11} first, then {4-7, 12-15}, matching which keys the two lane
-// halves hold in the 32x32 C layout.
-__device__ __forceinline__ int vperm16(int w) {
-    return (w & 3) + 4 * ((w >> 3) & 1) + 8 * ((w >> 2) & 1);
+typedef short s16x4_v __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed 16-bit pair with the hardware RNE converters.
+template <typename QT> __device__ __forceinline__ uint32_t cvt_pk(float a, float b);
+template <> __device__ __forceinline__ uint32_t cvt_pk<bf16_t>(float a, float b) {
+    f32x2_v v = {a, b};
+    bf16x2_v r = __builtin_convertvector(v, bf16x2_v);
+    return __builtin_bit_cast(uint32_t, r);
+}
+template <> __device__ __forceinline__ uint32_t cvt_pk<f16_t>(float a, float b) {
+    f32x2_v v = {a, b};
+    f16x2_v r = __builtin_convertvector(v, f16x2_v);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Tile geometry.  A K or V tile is 64 keys x D in LDS.  Copy instruction i
+// (i < NR = D/8) of a tile moves rows i, i + NR, i + 2 NR, ... (RPI = 64/NR
+// rows, one 1 KB run) into LDS block i; blocks are padded (K by 16 B, V by
+// 32 B) so the 32-row K operand reads and the 4-row transposing V reads hit
+// distinct banks.  Row r therefore lives at (r % NR) * BLK + (r / NR) * ROWB,
+// and every inner-loop LDS offset is an immediate on one per-lane base.
+template <int D> struct Tile {
+    static constexpr int ROWB = 2 * D;        // bytes per key row
+    static constexpr int NR = D / 8;          // copy instructions (= 1 KB blocks) per tile
+    static constexpr int RPI = 64 / NR;       // rows per copy instruction
+    static constexpr int KBLK = 1024 + 16;
+    static constexpr int VBLK = 1024 + 32;
+    static constexpr int KBYTES = NR * KBLK;
+    static constexpr int VBYTES = NR * VBLK;
+    static constexpr int STAGE = KBYTES + VBYTES;
+    static constexpr int NI = NR / 4;         // copy instructions per wave (K and V each)
+    static __device__ __forceinline__ int koff(int r) { return (r % NR) * KBLK + (r / NR) * ROWB; }
+    static __device__ __forceinline__ int voff(int r) { return (r % NR) * VBLK + (r / NR) * ROWB; }
+};
+
+// Buffer resource for a tile base that is uniform across the wave (forced
+// into SGPRs: the base can come from a block-table load the compiler cannot
+// prove uniform).  Reads past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint8_t* base, int bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+    void* u = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, static_cast<short>(0), bytes, 0x00020000);
 }
 
 template <typename QT, int D, bool FUSED>
 __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
     typedef typename Mfma32<QT>::op op_t;
-    constexpr int KS = D / 16;        // QK^T k-steps
+    typedef Tile<D> T;
+    constexpr int KS = D / 16;        // QK^T k-steps (16 dims each)
     constexpr int DB = D / 32;        // 32-dim output blocks
-    constexpr int KROW = D + 8;       // K tile row stride (elements), 16 B pad
-    constexpr int VROW = 64 + 8;      // V^T tile row stride (elements)
-    constexpr int CPR = D / 8;        // 16-byte chunks per row
-    constexpr int LPT = D / 32;       // 16-byte chunks per thread per tile (K and V each)
+    // [stage][K | V] tiles; stage 0 also holds the query rows in the prologue
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * T::STAGE];
 
-    __shared__ __attribute__((aligned(16))) uint16_t k_s[64 * KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t vt_s[D * VROW];
-
-    const int qt = p.nqt - 1 - static_cast<int>(blockIdx.x);
-    const int h = blockIdx.y, b = blockIdx.z;
+    // ---- work item: XCD-aware (WG i runs on XCD i % 8): all query tiles of
+    // the heads sharing a kv head land on the same XCD (its L2 keeps that kv
+    // head's K/V); within an XCD, query tiles run longest first.
+    int qt, h;
+    {
+        const int bid = blockIdx.x;
+        const int hpx = p.Hq / 8;  // heads per XCD when Hq % 8 == 0
+        if (hpx > 0 && (p.Hq % 8) == 0) {
+            const int xcd = bid & 7, slot = bid >> 3;
+            qt = p.nqt - 1 - slot / hpx;
+            h = xcd * hpx + slot % hpx;
+        } else {
+            qt = p.nqt - 1 - bid / p.Hq;
+            h = bid % p.Hq;
+        }
+    }
+    const int b = blockIdx.y;
     const int kvh = h / p.G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5;
@@ -112,74 +166,91 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
     const int lim_wave = min(L, off + min(row_w0 + 32, S));
     const int lim_row = min(L, off + myrow + 1);
 
-    // ------------------------------------------------ Q^T operand (registers)
-    op_t qb[KS];
-    {
-        const uint16_t* qrow = p.q + b * p.q_bs + h * p.q_hs + static_cast<int64_t>(row_ok ? myrow : 0) * p.q_rs;
-        u32x4_v raw[KS];
+    // Direct global->LDS copy of key tile `it` into stage `st` (asynchronous,
+    // counted by vmcnt).  Lane l of copy instruction i moves 16 bytes of row
+    // i + NR (l / (D/8)); rows past kv_len fall outside the buffer range and
+    // read as zeros (masked later; never stale cache contents).
+    const int dma_lane = (lane / (D / 8)) * T::NR * T::ROWB + (lane % (D / 8)) * 16;
+    auto issue_tile = [&](int it, int st) {
+        const int k0 = it * 64;
+        const int64_t base = p.kv.row(b, kvh, k0, D) * 2;  // a tile lies inside one page
+        const int bytes = min(64, L - k0) * T::ROWB;
+        const __amdgpu_buffer_rsrc_t kr = tile_rsrc(p.kv.k + base, bytes);
+        const __amdgpu_buffer_rsrc_t vr = tile_rsrc(p.kv.v + base, bytes);
+        // LDS destinations go to M0: keep them visibly wave-uniform
+        const int lbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + wave * T::NI * T::KBLK);
+        const int vbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + T::KBYTES + wave * T::NI * T::VBLK);
+        uint8_t* kl = lds + lbase;
+        uint8_t* vl = lds + vbase;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            raw[s] = row_ok ? ld16(qrow + 16 * s + 8 * g) : u32x4_v{0u, 0u, 0u, 0u};
+        for (int j = 0; j < T::NI; ++j) {
+            const int i = wave * T::NI + j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)(kl + j * T::KBLK), 16,
+                                                     dma_lane, i * T::ROWB, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(vl + j * T::VBLK), 16,
+                                                     dma_lane, i * T::ROWB, 0, 0);
         }
-        if constexpr (FUSED) {
-            // RMSNorm with (1 + w) and rotate-half RoPE at position off + row,
-            // bf16 after each step (prefill_engine.rs:2025-2096).  Values stay
-            // packed in `raw` between the steps to keep register pressure low.
+    };
+    if (ntiles > 0) issue_tile(0, 1);
+
+    // ------------------------------------------------ Q^T operand (registers)
+    // B operand of S^T = K Q^T: lane holds query row (lane & 31), dims 16 s + 8 g + j.
+    op_t qb[KS];
+    if constexpr (!FUSED) {
+        const uint16_t* qrow = p.q + b * p.q_bs + h * p.q_hs + static_cast<int64_t>(row_ok ? myrow : 0) * p.q_rs;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            qb[s] = to_op<op_t>(row_ok ? ld16(qrow + 16 * s + 8 * g) : u32x4_v{0u, 0u, 0u, 0u});
+    } else {
+        // Stage this wave's 32 query rows in LDS (buffer 0), then RMSNorm with
+        // (1 + w) and rotate-half RoPE at position off + row, bf16 after each
+        // step (prefill_engine.rs:2025-2096), then read the operand back.
+        uint16_t* qs = reinterpret_cast<uint16_t*>(lds) + wave * 32 * D;
+        constexpr int LPR = D / 8;              // lanes per row, 16 B each
+        constexpr int RPI = 64 / LPR;           // rows per instruction
+        for (int r0 = 0; r0 < 32; r0 += RPI) {
+            const int r = r0 + lane / LPR, c = lane % LPR;
+            const int row = row_w0 + r;
+            u32x4_v w = {0u, 0u, 0u, 0u};
+            if (row < S) w = ld16(p.q + h * p.q_hs + static_cast<int64_t>(row) * p.q_rs + 8 * c);
+            float x[8];
+            unpack8<bf16_t>(w, x);
             float ss = 0.f;
 #pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                float x[8];
-                unpack8<bf16_t>(raw[s], x);
+            for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
-            }
-            ss += __shfl_xor(ss, 32);
+            for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
             const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
+            float wt[8];
+            unpack8<bf16_t>(ld16(p.q_norm_w + 8 * c), wt);
+            u32x4_v o;
 #pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                float x[8], w[8];
-                unpack8<bf16_t>(raw[s], x);
-                unpack8<bf16_t>(ld16(p.q_norm_w + 16 * s + 8 * g), w);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    raw[s][j] = pk2<bf16_t>(x[2 * j] * inv * (w[2 * j] + 1.0f),
-                                            x[2 * j + 1] * inv * (w[2 * j + 1] + 1.0f));
-            }
-            const int hr = p.half_rot;  // multiple of 16 (checked on the host)
-            if (hr > 0 && row_ok) {
-                const int pos = off + myrow;
-                const int sh = hr / 16;
-#pragma unroll
-                for (int s = 0; s < KS / 2; ++s) {
-                    if (s < sh) {
-                        float c[8], sn[8], x0[8], x1[8];
-                        unpack8<bf16_t>(ld16(p.cos_t + static_cast<int64_t>(pos) * hr + 16 * s + 8 * g), c);
-                        unpack8<bf16_t>(ld16(p.sin_t + static_cast<int64_t>(pos) * hr + 16 * s + 8 * g), sn);
-                        unpack8<bf16_t>(raw[s], x0);
-                        u32x4_v hi = raw[0];
-#pragma unroll
-                        for (int s2 = 0; s2 < KS; ++s2)
-                            if (s2 == s + sh) hi = raw[s2];
-                        unpack8<bf16_t>(hi, x1);
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            raw[s][j] = pk2<bf16_t>(x0[2 * j] * c[2 * j] - x1[2 * j] * sn[2 * j],
-                                                    x0[2 * j + 1] * c[2 * j + 1] - x1[2 * j + 1] * sn[2 * j + 1]);
-                            hi[j] = pk2<bf16_t>(x0[2 * j] * sn[2 * j] + x1[2 * j] * c[2 * j],
-                                                x0[2 * j + 1] * sn[2 * j + 1] + x1[2 * j + 1] * c[2 * j + 1]);
-                        }
-#pragma unroll
-                        for (int s2 = 0; s2 < KS; ++s2)
-                            if (s2 == s + sh) raw[s2] = hi;
-                    }
-                }
-            }
-#pragma unroll
-            for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(raw[s]);
-        } else {
-#pragma unroll
-            for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(raw[s]);
+            for (int j = 0; j < 4; ++j)
+                o[j] = pk2<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
+            st16(qs + r * D + 8 * c, o);
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int hr = p.half_rot;
+        for (int idx = lane; idx < 32 * hr; idx += 64) {
+            const int r = idx / hr, i = idx % hr;
+            const int row = row_w0 + r;
+            if (row < S) {
+                const int pos = off + row;
+                const float c = bf16_bits_to_f32(p.cos_t[static_cast<int64_t>(pos) * hr + i]);
+                const float sn = bf16_bits_to_f32(p.sin_t[static_cast<int64_t>(pos) * hr + i]);
+                const float x0 = bf16_bits_to_f32(qs[r * D + i]);
+                const float x1 = bf16_bits_to_f32(qs[r * D + i + hr]);
+                qs[r * D + i] = static_cast<uint16_t>(f32_to_bf16_bits(x0 * c - x1 * sn));
+                qs[r * D + i + hr] = static_cast<uint16_t>(f32_to_bf16_bits(x0 * sn + x1 * c));
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(ld16(qs + (lane & 31) * D + 16 * s + 8 * g));
     }
 
     f32x16_v oacc[DB];
@@ -188,68 +259,45 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
     float m_run = -1e30f, l_part = 0.f;
+    const float c2 = p.scale_log2;
 
-    // ------------------------------------------------ tile loads
-    u32x4_v kreg[LPT], vreg[LPT];
-    auto load_tile = [&](int k0) {
-        const int64_t base = p.kv.row(b, kvh, k0, D);  // tile lies inside one page
-        const int last = L - 1 - k0;
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int ci = tid + 256 * i;
-            const int tok = min(ci / CPR, last);
-            const int c = ci % CPR;
-            kreg[i] = ld16(p.kv.k + (base + static_cast<int64_t>(tok) * D + 8 * c) * 2);
-        }
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int tok = min(tid & 63, last);
-            const int c = (tid >> 6) + 4 * i;
-            vreg[i] = ld16(p.kv.v + (base + static_cast<int64_t>(tok) * D + 8 * c) * 2);
-        }
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int ci = tid + 256 * i;
-            const int tok = ci / CPR;
-            const int c = ci % CPR;
-            st16(&k_s[tok * KROW + 8 * c], kreg[i]);
-        }
-        const int tok = tid & 63;
-        const int vp = (tok & ~15) + vperm16(tok & 15);
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int c = (tid >> 6) + 4 * i;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vt_s[(8 * c + 2 * e) * VROW + vp] = static_cast<uint16_t>(vreg[i][e] & 0xFFFFu);
-                vt_s[(8 * c + 2 * e + 1) * VROW + vp] = static_cast<uint16_t>(vreg[i][e] >> 16);
-            }
-        }
-    };
-
-    if (ntiles > 0) load_tile(0);
     for (int it = 0; it < ntiles; ++it) {
         const int k0 = it * 64;
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        if (it + 1 < ntiles) load_tile(k0 + 64);
-        if (k0 >= lim_wave) continue;  // the whole tile is past this wave's rows
+        const int st = (it + 1) & 1;
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile `it` have landed
+        __syncthreads();                // ... and everyone's; stage st^1 is free again
+        if (it + 1 < ntiles) issue_tile(it + 1, st ^ 1);
+        if (k0 >= lim_wave) continue;   // the whole tile is past this wave's rows
 
-        // S^T = K Q^T for the two 32-key blocks.
+        const uint8_t* kl = lds + st * T::STAGE + T::koff(lane & 31) + 16 * g;
+        const uint8_t* vl = lds + st * T::STAGE + T::KBYTES + 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3));
+        const int vrow = 4 * g + ((lane & 15) >> 2);
+
+        // S^T = K Q^T, the two 32-key blocks interleaved.
         f32x16_v sacc[2];
 #pragma unroll
-        for (int bt = 0; bt < 2; ++bt) {
+        for (int bt = 0; bt < 2; ++bt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) sacc[bt][i] = 0.f;
-            const uint16_t* kr = &k_s[(32 * bt + (lane & 31)) * KROW + 8 * g];
 #pragma unroll
-            for (int s = 0; s < KS; ++s) sacc[bt] = Mfma32<QT>::mma(to_op<op_t>(ld16(kr + 16 * s)), qb[s], sacc[bt]);
+        for (int s = 0; s < KS; ++s) {
+#pragma unroll
+            for (int bt = 0; bt < 2; ++bt) {
+                const op_t ka = to_op<op_t>(ld16(kl + (T::koff(32 * bt + 31) - T::koff(31)) + 32 * s));
+                sacc[bt] = Mfma32<QT>::mma(ka, qb[s], sacc[bt]);
+            }
         }
+        // keep 6 K-operand reads in flight ahead of the MFMA chain
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * KS - 6; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+        __builtin_amdgcn_sched_barrier(0);  // QK^T phase ends here
 
-        // Online softmax (base 2).  Lane holds row myrow, keys
+        // Online softmax, base 2.  Lane holds row myrow and keys
         // k0 + 32 bt + 8 (i>>2) + 4 g + (i&3).
         const bool need_mask = (k0 + 64 > off + row_w0 + 1) || (k0 + 64 > L);
         float mx = -INFINITY;
@@ -257,7 +305,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
         for (int bt = 0; bt < 2; ++bt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float v = sacc[bt][i] * p.scale_log2;
+                float v = sacc[bt][i];
                 if (need_mask) {
                     const int t = k0 + 32 * bt + 8 * (i >> 2) + 4 * g + (i & 3);
                     if (t >= lim_row) v = -INFINITY;
@@ -265,10 +313,22 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
                 sacc[bt][i] = v;
                 mx = fmaxf(mx, v);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = exp2f(m_run - m_new);
-        m_run = m_new;
+        mx = fmaxf(mx, __shfl_xor(mx, 32)) * c2;
+        // The running max m_run moves only when a row's max exceeds it by more
+        // than rescale_slack (log2 units); the AGPR-resident O is rescaled in a
+        // wave-uniform branch.  With slack 0 every row's largest weight is
+        // exactly 1 (no bf16 rounding on the dominant term).
+        if (__any(mx > m_run + p.rescale_slack)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_part *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+        }
+        const float m_use = m_run;
         float psum = 0.f;
         op_t pk[4];
 #pragma unroll
@@ -276,26 +336,45 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
             u32x4_v w;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float a = exp2f(sacc[u >> 1][8 * (u & 1) + 2 * j] - m_new);
-                const float c = exp2f(sacc[u >> 1][8 * (u & 1) + 2 * j + 1] - m_new);
+                const float a = __builtin_amdgcn_exp2f(fmaf(sacc[u >> 1][8 * (u & 1) + 2 * j], c2, -m_use));
+                const float c = __builtin_amdgcn_exp2f(fmaf(sacc[u >> 1][8 * (u & 1) + 2 * j + 1], c2, -m_use));
                 psum += a + c;
-                w[j] = pk2<QT>(a, c);
+                w[j] = cvt_pk<QT>(a, c);
             }
             pk[u] = to_op<op_t>(w);
         }
-        l_part = l_part * alpha + psum;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+        l_part += psum;
 
-        // O^T += V^T P^T.
+        __builtin_amdgcn_sched_barrier(0);  // softmax phase ends here
+        // O^T += V^T P^T; V^T operands come from transposing LDS reads: the 16
+        // lanes of a group read 4 keys x 16 dims and each lane receives 4
+        // consecutive keys of one dim.
+        // Lane base: key 4 g + ((lane & 15) >> 2), dim 16 ((lane >> 4) & 1) + 4 (lane & 3);
+        // block u = 2 bt + h adds 16 u keys, the second read 8 more, db adds 32 dims.
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-            const uint16_t* vr = &vt_s[(32 * db + (lane & 31)) * VROW + 8 * g];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) oacc[db] = Mfma32<QT>::mma(to_op<op_t>(ld16(vr + 16 * u)), pk[u], oacc[db]);
+            for (int u = 0; u < 4; ++u) {
+                const s16x4_v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(vrow + 16 * u) + 64 * db));
+                const s16x4_v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(vrow + 16 * u + 8) + 64 * db));
+                u32x4_v w;
+                w[0] = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
+                w[1] = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
+                w[2] = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
+                w[3] = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
+                oacc[db] = Mfma32<QT>::mma(to_op<op_t>(w), pk[u], oacc[db]);
+            }
         }
+        // keep 4 V-operand (2 transposing reads each) fetches ahead of the MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+#pragma unroll
+        for (int i = 0; i < 4 * DB - 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
     }
 
     // ------------------------------------------------ epilogue
@@ -335,6 +414,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
                 *reinterpret_cast<u32x2_v*>(orow + d) = o;
             }
     }
+#endif
 }
 
 // ----------------------------------------------------------------------------
@@ -486,6 +566,11 @@ static hipError_t launch_prefill(int D, dim3 grid, hipStream_t st, const Prefill
     return hipGetLastError();
 }
 
+static float rescale_slack() {
+    const char* v = getenv("SUPERSONIC_PREFILL_RESCALE_SLACK");
+    return (v && *v) ? static_cast<float>(atof(v)) : 0.0f;
+}
+
 static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t Hkv, size_t q_len, size_t kv_len,
                           size_t D, size_t groups, float scale, size_t off, const void* q, const void* k,
                           const void* v, void* out) {
@@ -521,12 +606,13 @@ static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t 
     p.L = static_cast<int>(kv_len);
     p.off = static_cast<int>(off);
     p.scale_log2 = scale * kLog2e;
+    p.rescale_slack = rescale_slack();
     p.nqt = static_cast<int>((q_len + 127) / 128);
     p.out_f32 = static_cast<float*>(out);
     p.o_rs = p.q_rs;
     p.o_hs = p.q_hs;
     p.o_bs = p.q_bs;
-    dim3 grid(p.nqt, static_cast<unsigned>(Hq), static_cast<unsigned>(B));
+    dim3 grid(p.nqt * static_cast<unsigned>(Hq), static_cast<unsigned>(B));
     const hipError_t e = dtype == 0 ? launch_prefill<f16_t, false>(static_cast<int>(D), grid, nullptr, p)
                                     : launch_prefill<bf16_t, false>(static_cast<int>(D), grid, nullptr, p);
     if (e != hipSuccess) return 11;
@@ -602,6 +688,7 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.L = static_cast<int>(chunk_start + chunk_len);
     p.off = static_cast<int>(chunk_start);
     p.scale_log2 = scale * kLog2e;
+    p.rescale_slack = rescale_slack();
     p.nqt = static_cast<int>((chunk_len + 127) / 128);
     p.out_bf16 = static_cast<uint16_t*>(out);
     p.gate = static_cast<const uint16_t*>(q_proj) + head_dim;
@@ -610,7 +697,7 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.sin_t = static_cast<const uint16_t*>(sin_table);
     p.half_rot = static_cast<int>(rotary_dim / 2);
     p.eps = eps;
-    dim3 grid(p.nqt, static_cast<unsigned>(q_heads), 1);
+    dim3 grid(p.nqt * static_cast<unsigned>(q_heads), 1);
     const ProfileEvents prof = take_profile_events();
     if (prof.before) (void)hipEventRecord(prof.before, st);
     if (launch_prefill<bf16_t, true>(static_cast<int>(head_dim), grid, st, p) != hipSuccess)
