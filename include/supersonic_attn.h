@@ -97,13 +97,13 @@ int supersonic_qwen35_4b_hip_quantize_kv_to_fp8(
 
 /* Row RMSNorm, x * rsqrt(mean(x^2) + eps) * (w [+ 1]).  Replaces
  * kernels/full_attention_bridge.cpp:3946 (kernel full_attention.hip:2507-2560),
- * bound at prefill_ffi.rs:637-647.  Status: 74 bad dtype, 71 launch, 72 sync. */
+ * bound at prefill_ffi.rs:638-648.  Status: 74 bad dtype, 71 launch, 72 sync. */
 int supersonic_qwen35_hip_rms_norm(
     int dtype, size_t device_ordinal, size_t n_rows, size_t n_cols, float eps,
     int add_unit_offset, const void* xs, const void* weight, void* out);
 
 /* Element cast.  Replaces kernels/full_attention_bridge.cpp:3563, bound at
- * prefill_ffi.rs:649-656.  Status: 137 bad dtype, 135 launch, 136 sync. */
+ * prefill_ffi.rs:650-657.  Status: 137 bad dtype, 135 launch, 136 sync. */
 int supersonic_qwen35_hip_cast(
     int input_dtype, int output_dtype, size_t device_ordinal, size_t total_elems,
     const void* xs, void* out);
@@ -111,27 +111,27 @@ int supersonic_qwen35_hip_cast(
 /* In-place partial RoPE on [seq_len, num_heads, head_dim]; cos/sin tables
  * [*, half_rot] already offset to the chunk's first position.  Replaces
  * kernels/prefill_helpers_bridge.cpp:293 (kernel prefill_helpers.hip:79-108),
- * bound at prefill_ffi.rs:669-679.  Status: 310 bad dtype, 311 launch, 312 sync. */
+ * bound at prefill_ffi.rs:670-680.  Status: 310 bad dtype, 311 launch, 312 sync. */
 int supersonic_qwen35_hip_apply_rope_prefill(
     int dtype, size_t device_ordinal, size_t seq_len, size_t num_heads, size_t head_dim,
     size_t half_rot, const void* cos_table, const void* sin_table, void* data);
 
 /* [S, H, D] -> [H, S, D].  Replaces kernels/prefill_helpers_bridge.cpp:315
- * (kernel prefill_helpers.hip:114-130), bound at prefill_ffi.rs:681-689.
+ * (kernel prefill_helpers.hip:114-130), bound at prefill_ffi.rs:682-690.
  * Status: 320 bad dtype, 321 launch, 322 sync. */
 int supersonic_qwen35_hip_transpose_shd_hsd(
     int dtype, size_t device_ordinal, size_t s, size_t h, size_t d, const void* src, void* dst);
 
 /* out = data * sigmoid(gate).  Replaces kernels/prefill_helpers_bridge.cpp:363
- * (kernel prefill_helpers.hip:183-195), bound at prefill_ffi.rs:691-698.
+ * (kernel prefill_helpers.hip:183-195), bound at prefill_ffi.rs:692-699.
  * Status: 350 bad dtype, 351 launch, 352 sync. */
 int supersonic_qwen35_hip_sigmoid_mul(
     int dtype, size_t device_ordinal, size_t total_elems, const void* data, const void* gate,
     void* out);
 
 /* [S, H, 2D] per-head [q | gate] -> query [S, H, D], gate [S, H, D].  Replaces
- * kernels/prefill_helpers_bridge.cpp (kernel prefill_helpers.hip:239-257), bound
- * at prefill_ffi.rs:713-722.  Status: 370 bad dtype, 371 launch, 372 sync. */
+ * kernels/prefill_helpers_bridge.cpp:393 (kernel prefill_helpers.hip:239-257), bound
+ * at prefill_ffi.rs:714-723.  Status: 370 bad dtype, 371 launch, 372 sync. */
 int supersonic_qwen35_hip_split_qgate(
     int dtype, size_t device_ordinal, size_t s, size_t num_heads, size_t head_dim,
     const void* src, void* query_out, void* gate_out);

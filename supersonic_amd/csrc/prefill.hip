@@ -96,16 +96,18 @@ template <> __device__ __forceinline__ uint32_t cvt_pk<f16_t>(float a, float b) 
 
 // Tile geometry.  A K or V tile is 64 keys x D in LDS.  Copy instruction i
 // (i < NR = D/8) of a tile moves rows i, i + NR, i + 2 NR, ... (RPI = 64/NR
-// rows, one 1 KB run) into LDS block i; blocks are padded (K by 16 B, V by
-// 32 B) so the 32-row K operand reads and the 4-row transposing V reads hit
-// distinct banks.  Row r therefore lives at (r % NR) * BLK + (r / NR) * ROWB,
+// rows, one 1 KB run) into LDS block i.  Blocks are padded so reads are
+// bank-conflict free on the 64 x 4-byte banks: K blocks by 4 words (the 16
+// rows of a 16-lane ds_read_b128 pass land 4 banks apart), V blocks by 16
+// words (a 32-lane half of a transposing read touches 4 rows x 2 dim groups x
+// 8 words = all 64 banks once).  Row r therefore lives at (r % NR) * BLK + (r / NR) * ROWB,
 // and every inner-loop LDS offset is an immediate on one per-lane base.
 template <int D> struct Tile {
     static constexpr int ROWB = 2 * D;        // bytes per key row
     static constexpr int NR = D / 8;          // copy instructions (= 1 KB blocks) per tile
     static constexpr int RPI = 64 / NR;       // rows per copy instruction
     static constexpr int KBLK = 1024 + 16;
-    static constexpr int VBLK = 1024 + 32;
+    static constexpr int VBLK = 1024 + 64;
     static constexpr int KBYTES = NR * KBLK;
     static constexpr int VBYTES = NR * VBLK;
     static constexpr int STAGE = KBYTES + VBYTES;
@@ -153,7 +155,8 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
     }
     const int b = blockIdx.y;
     const int kvh = h / p.G;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps copy offsets in SGPRs
     const int g = lane >> 5;
     const int q0 = qt * 128;
     const int row_w0 = q0 + 32 * wave;
@@ -360,10 +363,12 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
                 const s16x4_v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                     (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(vrow + 16 * u + 8) + 64 * db));
                 u32x4_v w;
-                w[0] = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
-                w[1] = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
-                w[2] = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
-                w[3] = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
+                const u32x2_v lw = __builtin_bit_cast(u32x2_v, lo);
+                const u32x2_v hw = __builtin_bit_cast(u32x2_v, hi);
+                w[0] = lw[0];
+                w[1] = lw[1];
+                w[2] = hw[0];
+                w[3] = hw[1];
                 oacc[db] = Mfma32<QT>::mma(to_op<op_t>(w), pk[u], oacc[db]);
             }
         }

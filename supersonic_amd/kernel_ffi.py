@@ -19,7 +19,7 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsupersonic_attn.so")
+LIB_PATH = os.environ.get("SUPERSONIC_ATTN_LIB") or os.path.join(HERE, "libsupersonic_attn.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "supersonic_attn.h")
 
 
