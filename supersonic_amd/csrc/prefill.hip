@@ -95,25 +95,30 @@ template <> __device__ __forceinline__ uint32_t cvt_pk<f16_t>(float a, float b) 
 }
 
 // Tile geometry.  A K or V tile is 64 keys x D in LDS.  Copy instruction i
-// (i < NR = D/8) of a tile moves rows i, i + NR, i + 2 NR, ... (RPI = 64/NR
-// rows, one 1 KB run) into LDS block i.  Blocks are padded so reads are
-// bank-conflict free on the 64 x 4-byte banks: K blocks by 4 words (the 16
-// rows of a 16-lane ds_read_b128 pass land 4 banks apart), V blocks by 16
-// words (a 32-lane half of a transposing read touches 4 rows x 2 dim groups x
-// 8 words = all 64 banks once).  Row r therefore lives at (r % NR) * BLK + (r / NR) * ROWB,
-// and every inner-loop LDS offset is an immediate on one per-lane base.
+// (i < NR = D/8) of a tile moves rows i, i + NR, i + 2 NR, ... (64/NR rows,
+// one 1 KB run) into LDS block i.  Blocks are padded so reads hit distinct
+// banks: K and V blocks by 8 words each (measured on gfx950 with
+// SQ_LDS_BANK_CONFLICT over pads of 4/8/16/32 words: 8/8 is the only pair
+// without conflicts for the 16-row ds_read_b128 K reads and the 4-row
+// transposing V reads).  Row r lives at (r % NR) * BLK + (r / NR) *
+// ROWB, so every inner-loop LDS offset is an immediate on one per-lane base.
 template <int D> struct Tile {
     static constexpr int ROWB = 2 * D;        // bytes per key row
     static constexpr int NR = D / 8;          // copy instructions (= 1 KB blocks) per tile
-    static constexpr int RPI = 64 / NR;       // rows per copy instruction
-    static constexpr int KBLK = 1024 + 16;
-    static constexpr int VBLK = 1024 + 64;
+#ifndef SSA_KPAD
+#define SSA_KPAD 32
+#endif
+#ifndef SSA_VPAD
+#define SSA_VPAD 32
+#endif
+    static constexpr int KBLK = 1024 + SSA_KPAD;
+    static constexpr int VBLK = 1024 + SSA_VPAD;
     static constexpr int KBYTES = NR * KBLK;
     static constexpr int VBYTES = NR * VBLK;
     static constexpr int STAGE = KBYTES + VBYTES;
-    static constexpr int NI = NR / 4;         // copy instructions per wave (K and V each)
-    static __device__ __forceinline__ int koff(int r) { return (r % NR) * KBLK + (r / NR) * ROWB; }
-    static __device__ __forceinline__ int voff(int r) { return (r % NR) * VBLK + (r / NR) * ROWB; }
+    static constexpr int NI = NR / 8;         // copy instructions per wave (K and V each), 8 waves
+    static __device__ __forceinline__ constexpr int koff(int r) { return (r % NR) * KBLK + (r / NR) * ROWB; }
+    static __device__ __forceinline__ constexpr int voff(int r) { return (r % NR) * VBLK + (r / NR) * ROWB; }
 };
 
 // Buffer resource for a tile base that is uniform across the wave (forced
@@ -127,23 +132,50 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint8_t* base,
     return __builtin_amdgcn_make_buffer_rsrc(u, static_cast<short>(0), bytes, 0x00020000);
 }
 
+template <typename QT> struct Mfma16;
+template <> struct Mfma16<bf16_t> {
+    typedef bf16x8_v op;
+    static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma16<f16_t> {
+    typedef f16x8_v op;
+    static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+constexpr int kPrefillWaves = 8;   // 8 wave64s x 16 query rows = 128 rows per workgroup
+
+// One workgroup = 128 query rows of one head; each wave owns 16 rows, so two
+// waves share a SIMD (about 200 registers each) and one wave's softmax VALU
+// work overlaps the other's MFMA chains.
+//
+//   S^T = K Q^T      v_mfma_f32_16x16x32: A = 16 key rows (LDS), B = Q^T (16
+//                    query rows, registers).  C: lane l holds query row l & 15
+//                    and keys 16 kb + 4 (l >> 4) + i of key block kb.
+//   O^T += V^T P^T   per 32-key step the B operand (P^T) is the lane's own 8
+//                    weights (keys 4 g + i of the two 16-key blocks), and the A
+//                    operand (V^T) comes from two transposing LDS reads, each
+//                    giving a lane 4 consecutive keys of dim (l & 15).
 template <typename QT, int D, bool FUSED>
-__global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
-    typedef typename Mfma32<QT>::op op_t;
+    typedef typename Mfma16<QT>::op op_t;
     typedef Tile<D> T;
-    constexpr int KS = D / 16;        // QK^T k-steps (16 dims each)
-    constexpr int DB = D / 32;        // 32-dim output blocks
+    constexpr int KS = D / 32;        // QK^T k-steps (32 dims each)
+    constexpr int DBK = D / 16;       // 16-dim output blocks
     // [stage][K | V] tiles; stage 0 also holds the query rows in the prologue
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * T::STAGE];
 
-    // ---- work item: XCD-aware (WG i runs on XCD i % 8): all query tiles of
-    // the heads sharing a kv head land on the same XCD (its L2 keeps that kv
-    // head's K/V); within an XCD, query tiles run longest first.
+    // Work item, XCD-aware (workgroup i runs on XCD i % 8): the heads sharing a
+    // kv head run on one XCD, whose L2 keeps that kv head's K/V; query tiles run
+    // longest first.
     int qt, h;
     {
         const int bid = blockIdx.x;
-        const int hpx = p.Hq / 8;  // heads per XCD when Hq % 8 == 0
+        const int hpx = p.Hq / 8;
         if (hpx > 0 && (p.Hq % 8) == 0) {
             const int xcd = bid & 7, slot = bid >> 3;
             qt = p.nqt - 1 - slot / hpx;
@@ -156,17 +188,17 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
     const int b = blockIdx.y;
     const int kvh = h / p.G;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps copy offsets in SGPRs
-    const int g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy offsets stay in SGPRs
+    const int g4 = lane >> 4;
     const int q0 = qt * 128;
-    const int row_w0 = q0 + 32 * wave;
-    const int myrow = row_w0 + (lane & 31);
+    const int row_w0 = q0 + 16 * wave;
+    const int myrow = row_w0 + (lane & 15);
     const bool row_ok = myrow < p.S;
     const int S = p.S, L = p.L, off = p.off;
 
     const int lim_wg = min(L, off + min(q0 + 128, S));
     const int ntiles = lim_wg > 0 ? (lim_wg + 63) / 64 : 0;
-    const int lim_wave = min(L, off + min(row_w0 + 32, S));
+    const int lim_wave = min(L, off + min(row_w0 + 16, S));
     const int lim_row = min(L, off + myrow + 1);
 
     // Direct global->LDS copy of key tile `it` into stage `st` (asynchronous,
@@ -180,38 +212,35 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
         const int bytes = min(64, L - k0) * T::ROWB;
         const __amdgpu_buffer_rsrc_t kr = tile_rsrc(p.kv.k + base, bytes);
         const __amdgpu_buffer_rsrc_t vr = tile_rsrc(p.kv.v + base, bytes);
-        // LDS destinations go to M0: keep them visibly wave-uniform
         const int lbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + wave * T::NI * T::KBLK);
         const int vbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + T::KBYTES + wave * T::NI * T::VBLK);
-        uint8_t* kl = lds + lbase;
-        uint8_t* vl = lds + vbase;
 #pragma unroll
         for (int j = 0; j < T::NI; ++j) {
             const int i = wave * T::NI + j;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)(kl + j * T::KBLK), 16,
-                                                     dma_lane, i * T::ROWB, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(vl + j * T::VBLK), 16,
-                                                     dma_lane, i * T::ROWB, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)(lds + lbase + j * T::KBLK),
+                                                     16, dma_lane, i * T::ROWB, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(lds + vbase + j * T::VBLK),
+                                                     16, dma_lane, i * T::ROWB, 0, 0);
         }
     };
     if (ntiles > 0) issue_tile(0, 1);
 
     // ------------------------------------------------ Q^T operand (registers)
-    // B operand of S^T = K Q^T: lane holds query row (lane & 31), dims 16 s + 8 g + j.
+    // B operand of S^T = K Q^T: lane holds query row (lane & 15), dims 32 s + 8 g4 + j.
     op_t qb[KS];
     if constexpr (!FUSED) {
         const uint16_t* qrow = p.q + b * p.q_bs + h * p.q_hs + static_cast<int64_t>(row_ok ? myrow : 0) * p.q_rs;
 #pragma unroll
         for (int s = 0; s < KS; ++s)
-            qb[s] = to_op<op_t>(row_ok ? ld16(qrow + 16 * s + 8 * g) : u32x4_v{0u, 0u, 0u, 0u});
+            qb[s] = to_op<op_t>(row_ok ? ld16(qrow + 32 * s + 8 * g4) : u32x4_v{0u, 0u, 0u, 0u});
     } else {
-        // Stage this wave's 32 query rows in LDS (buffer 0), then RMSNorm with
+        // Stage this wave's 16 query rows in LDS (stage 0), RMSNorm with
         // (1 + w) and rotate-half RoPE at position off + row, bf16 after each
         // step (prefill_engine.rs:2025-2096), then read the operand back.
-        uint16_t* qs = reinterpret_cast<uint16_t*>(lds) + wave * 32 * D;
+        uint16_t* qs = reinterpret_cast<uint16_t*>(lds) + wave * 16 * D;
         constexpr int LPR = D / 8;              // lanes per row, 16 B each
         constexpr int RPI = 64 / LPR;           // rows per instruction
-        for (int r0 = 0; r0 < 32; r0 += RPI) {
+        for (int r0 = 0; r0 < 16; r0 += RPI) {
             const int r = r0 + lane / LPR, c = lane % LPR;
             const int row = row_w0 + r;
             u32x4_v w = {0u, 0u, 0u, 0u};
@@ -236,7 +265,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const int hr = p.half_rot;
-        for (int idx = lane; idx < 32 * hr; idx += 64) {
+        for (int idx = lane; idx < 16 * hr; idx += 64) {
             const int r = idx / hr, i = idx % hr;
             const int row = row_w0 + r;
             if (row < S) {
@@ -253,16 +282,21 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(ld16(qs + (lane & 31) * D + 16 * s + 8 * g));
+        for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(ld16(qs + (lane & 15) * D + 32 * s + 8 * g4));
     }
 
-    f32x16_v oacc[DB];
+    f32x4_v oacc[DBK];
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
+    for (int d = 0; d < DBK; ++d) oacc[d] = f32x4_v{0.f, 0.f, 0.f, 0.f};
     float m_run = -1e30f, l_part = 0.f;
     const float c2 = p.scale_log2;
+
+    // Per-lane LDS bases: K row (lane & 15), dims 8 g4; V row (key) 4 g4 +
+    // ((lane & 15) >> 2), dims 4 (lane & 3).  For r < 16, koff(r + 16 m) -
+    // koff(r) and voff(r + 16 m) - voff(r) do not depend on r, so the other
+    // rows are the compile-time offsets koff(16 m), voff(16 m).
+    const int kbase_off = T::koff(lane & 15) + 16 * g4;
+    const int vbase_off = T::KBYTES + T::voff(4 * g4 + ((lane & 15) >> 2)) + 2 * 4 * (lane & 3);
 
     for (int it = 0; it < ntiles; ++it) {
         const int k0 = it * 64;
@@ -272,110 +306,97 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
         if (it + 1 < ntiles) issue_tile(it + 1, st ^ 1);
         if (k0 >= lim_wave) continue;   // the whole tile is past this wave's rows
 
-        const uint8_t* kl = lds + st * T::STAGE + T::koff(lane & 31) + 16 * g;
-        const uint8_t* vl = lds + st * T::STAGE + T::KBYTES + 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3));
-        const int vrow = 4 * g + ((lane & 15) >> 2);
+        const uint8_t* kl = lds + st * T::STAGE + kbase_off;
+        const uint8_t* vl = lds + st * T::STAGE + vbase_off;
 
-        // S^T = K Q^T, the two 32-key blocks interleaved.
-        f32x16_v sacc[2];
+        // S^T = K Q^T, four 16-key blocks.
+        f32x4_v sacc[4];
 #pragma unroll
-        for (int bt = 0; bt < 2; ++bt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sacc[bt][i] = 0.f;
+        for (int kb = 0; kb < 4; ++kb) sacc[kb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
 #pragma unroll
-            for (int bt = 0; bt < 2; ++bt) {
-                const op_t ka = to_op<op_t>(ld16(kl + (T::koff(32 * bt + 31) - T::koff(31)) + 32 * s));
-                sacc[bt] = Mfma32<QT>::mma(ka, qb[s], sacc[bt]);
+            for (int kb = 0; kb < 4; ++kb) {
+                const op_t ka = to_op<op_t>(ld16(kl + T::koff(16 * kb) + 64 * s));
+                sacc[kb] = Mfma16<QT>::mma(ka, qb[s], sacc[kb]);
             }
         }
-        // keep 6 K-operand reads in flight ahead of the MFMA chain
         __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
-        for (int i = 0; i < 2 * KS - 6; ++i) {
+        for (int i = 0; i < 4 * KS - 6; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
-        __builtin_amdgcn_sched_barrier(0);  // QK^T phase ends here
+        __builtin_amdgcn_sched_barrier(0);
 
-        // Online softmax, base 2.  Lane holds row myrow and keys
-        // k0 + 32 bt + 8 (i>>2) + 4 g + (i&3).
+        // Online softmax, base 2, exact running max.  Lane holds row myrow and
+        // keys k0 + 16 kb + 4 g4 + i.
         const bool need_mask = (k0 + 64 > off + row_w0 + 1) || (k0 + 64 > L);
         float mx = -INFINITY;
 #pragma unroll
-        for (int bt = 0; bt < 2; ++bt)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float v = sacc[bt][i];
+            for (int i = 0; i < 4; ++i) {
+                float v = sacc[kb][i];
                 if (need_mask) {
-                    const int t = k0 + 32 * bt + 8 * (i >> 2) + 4 * g + (i & 3);
+                    const int t = k0 + 16 * kb + 4 * g4 + i;
                     if (t >= lim_row) v = -INFINITY;
                 }
-                sacc[bt][i] = v;
+                sacc[kb][i] = v;
                 mx = fmaxf(mx, v);
             }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32)) * c2;
-        // The running max m_run moves only when a row's max exceeds it by more
-        // than rescale_slack (log2 units); the AGPR-resident O is rescaled in a
-        // wave-uniform branch.  With slack 0 every row's largest weight is
-        // exactly 1 (no bf16 rounding on the dominant term).
         if (__any(mx > m_run + p.rescale_slack)) {
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
             l_part *= alpha;
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
+            for (int d = 0; d < DBK; ++d)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+                for (int i = 0; i < 4; ++i) oacc[d][i] *= alpha;
         }
         const float m_use = m_run;
         float psum = 0.f;
-        op_t pk[4];
+        op_t pk[2];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 2; ++u) {
             u32x4_v w;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float a = __builtin_amdgcn_exp2f(fmaf(sacc[u >> 1][8 * (u & 1) + 2 * j], c2, -m_use));
-                const float c = __builtin_amdgcn_exp2f(fmaf(sacc[u >> 1][8 * (u & 1) + 2 * j + 1], c2, -m_use));
-                psum += a + c;
-                w[j] = cvt_pk<QT>(a, c);
-            }
+            for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float a = __builtin_amdgcn_exp2f(fmaf(sacc[2 * u + hb][2 * j], c2, -m_use));
+                    const float c = __builtin_amdgcn_exp2f(fmaf(sacc[2 * u + hb][2 * j + 1], c2, -m_use));
+                    psum += a + c;
+                    w[2 * hb + j] = cvt_pk<QT>(a, c);
+                }
             pk[u] = to_op<op_t>(w);
         }
         l_part += psum;
+        __builtin_amdgcn_sched_barrier(0);
 
-        __builtin_amdgcn_sched_barrier(0);  // softmax phase ends here
-        // O^T += V^T P^T; V^T operands come from transposing LDS reads: the 16
-        // lanes of a group read 4 keys x 16 dims and each lane receives 4
-        // consecutive keys of one dim.
-        // Lane base: key 4 g + ((lane & 15) >> 2), dim 16 ((lane >> 4) & 1) + 4 (lane & 3);
-        // block u = 2 bt + h adds 16 u keys, the second read 8 more, db adds 32 dims.
+        // O^T += V^T P^T: two 32-key steps; A operand rows (keys) 32 u + 4 g4
+        // + {0..3} and 32 u + 16 + 4 g4 + {0..3}, dim 16 d + (lane & 15).
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
+        for (int d = 0; d < DBK; ++d) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < 2; ++u) {
                 const s16x4_v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(vrow + 16 * u) + 64 * db));
+                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(32 * u) + 32 * d));
                 const s16x4_v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(vrow + 16 * u + 8) + 64 * db));
-                u32x4_v w;
+                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(32 * u + 16) + 32 * d));
                 const u32x2_v lw = __builtin_bit_cast(u32x2_v, lo);
                 const u32x2_v hw = __builtin_bit_cast(u32x2_v, hi);
-                w[0] = lw[0];
-                w[1] = lw[1];
-                w[2] = hw[0];
-                w[3] = hw[1];
-                oacc[db] = Mfma32<QT>::mma(to_op<op_t>(w), pk[u], oacc[db]);
+                const u32x4_v w = {lw[0], lw[1], hw[0], hw[1]};
+                oacc[d] = Mfma16<QT>::mma(to_op<op_t>(w), pk[u], oacc[d]);
             }
         }
-        // keep 4 V-operand (2 transposing reads each) fetches ahead of the MFMAs
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
 #pragma unroll
-        for (int i = 0; i < 4 * DB - 4; ++i) {
+        for (int i = 0; i < 2 * DBK - 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
         }
@@ -383,41 +404,37 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
     }
 
     // ------------------------------------------------ epilogue
-    const float l_tot = l_part + __shfl_xor(l_part, 32);
+    // O^T C layout: lane holds row myrow, dims 16 d + 4 g4 + i.
+    float l_tot = l_part + __shfl_xor(l_part, 16);
+    l_tot += __shfl_xor(l_tot, 32);
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     if (!row_ok) return;
     if constexpr (!FUSED) {
         float* orow = p.out_f32 + b * p.o_bs + h * p.o_hs + static_cast<int64_t>(myrow) * p.o_rs;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const int d = 32 * db + 8 * q4 + 4 * g;
-                f32x4_v o = {oacc[db][4 * q4] * inv, oacc[db][4 * q4 + 1] * inv, oacc[db][4 * q4 + 2] * inv,
-                             oacc[db][4 * q4 + 3] * inv};
-                *reinterpret_cast<f32x4_v*>(orow + d) = o;
-            }
+        for (int d = 0; d < DBK; ++d) {
+            f32x4_v o = {oacc[d][0] * inv, oacc[d][1] * inv, oacc[d][2] * inv, oacc[d][3] * inv};
+            *reinterpret_cast<f32x4_v*>(orow + 16 * d + 4 * g4) = o;
+        }
     } else {
         // bf16(attn) * sigmoid(gate), bf16 out [S, Hq*D] (prefill_engine.rs:2263-2308).
         uint16_t* orow = p.out_bf16 + static_cast<int64_t>(myrow) * p.Hq * D + h * D;
         const uint16_t* grow = p.gate + h * p.q_hs + static_cast<int64_t>(myrow) * p.q_rs;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
+        for (int d = 0; d < DBK; ++d) {
+            const int dd = 16 * d + 4 * g4;
+            const u32x2_v gw = *reinterpret_cast<const u32x2_v*>(grow + dd);
+            const float gv[4] = {bf16_bits_to_f32(gw[0] & 0xFFFFu), bf16_bits_to_f32(gw[0] >> 16),
+                                 bf16_bits_to_f32(gw[1] & 0xFFFFu), bf16_bits_to_f32(gw[1] >> 16)};
+            uint32_t r[4];
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const int d = 32 * db + 8 * q4 + 4 * g;
-                const u32x2_v gw = *reinterpret_cast<const u32x2_v*>(grow + d);
-                float gv[4] = {bf16_bits_to_f32(gw[0] & 0xFFFFu), bf16_bits_to_f32(gw[0] >> 16),
-                               bf16_bits_to_f32(gw[1] & 0xFFFFu), bf16_bits_to_f32(gw[1] >> 16)};
-                uint32_t r[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float a = bf16_round(oacc[db][4 * q4 + e] * inv);
-                    r[e] = f32_to_bf16_bits(a * (1.0f / (1.0f + expf(-gv[e]))));
-                }
-                u32x2_v o = {r[0] | (r[1] << 16), r[2] | (r[3] << 16)};
-                *reinterpret_cast<u32x2_v*>(orow + d) = o;
+            for (int e = 0; e < 4; ++e) {
+                const float a = bf16_round(oacc[d][e] * inv);
+                r[e] = f32_to_bf16_bits(a * (1.0f / (1.0f + expf(-gv[e]))));
             }
+            const u32x2_v o = {r[0] | (r[1] << 16), r[2] | (r[3] << 16)};
+            *reinterpret_cast<u32x2_v*>(orow + dd) = o;
+        }
     }
 #endif
 }
@@ -563,9 +580,9 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(KvPrepParams p) {
 template <typename QT, bool FUSED>
 static hipError_t launch_prefill(int D, dim3 grid, hipStream_t st, const PrefillParams& p) {
     switch (D) {
-    case 64: hipLaunchKernelGGL((prefill_kernel<QT, 64, FUSED>), grid, dim3(256), 0, st, p); break;
-    case 128: hipLaunchKernelGGL((prefill_kernel<QT, 128, FUSED>), grid, dim3(256), 0, st, p); break;
-    case 256: hipLaunchKernelGGL((prefill_kernel<QT, 256, FUSED>), grid, dim3(256), 0, st, p); break;
+    case 64: hipLaunchKernelGGL((prefill_kernel<QT, 64, FUSED>), grid, dim3(64 * kPrefillWaves), 0, st, p); break;
+    case 128: hipLaunchKernelGGL((prefill_kernel<QT, 128, FUSED>), grid, dim3(64 * kPrefillWaves), 0, st, p); break;
+    case 256: hipLaunchKernelGGL((prefill_kernel<QT, 256, FUSED>), grid, dim3(64 * kPrefillWaves), 0, st, p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
