@@ -105,6 +105,13 @@ template <> __device__ __forceinline__ uint32_t cvt_pk<f16_t>(float a, float b) 
 template <int D> struct Tile {
     static constexpr int ROWB = 2 * D;        // bytes per key row
     static constexpr int NR = D / 8;          // copy instructions (= 1 KB blocks) per tile
+// LDS read lookahead of the K-operand (reads) and V-operand (MFMAs) pipelines
+#ifndef SSA_KLA
+#define SSA_KLA 6
+#endif
+#ifndef SSA_VLA
+#define SSA_VLA 4
+#endif
 #ifndef SSA_KPAD
 #define SSA_KPAD 32
 #endif
@@ -321,13 +328,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillPara
                 sacc[kb] = Mfma16<QT>::mma(ka, qb[s], sacc[kb]);
             }
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, SSA_KLA, 0);
 #pragma unroll
-        for (int i = 0; i < 4 * KS - 6; ++i) {
+        for (int i = 0; i < 4 * KS - SSA_KLA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, SSA_KLA, 0);
         __builtin_amdgcn_sched_barrier(0);
 
         // Online softmax, base 2, exact running max.  Lane holds row myrow and
@@ -394,13 +401,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillPara
                 oacc[d] = Mfma16<QT>::mma(to_op<op_t>(w), pk[u], oacc[d]);
             }
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * SSA_VLA, 1);
 #pragma unroll
-        for (int i = 0; i < 2 * DBK - 4; ++i) {
+        for (int i = 0; i < 2 * DBK - SSA_VLA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, SSA_VLA, 1);
     }
 
     // ------------------------------------------------ epilogue
