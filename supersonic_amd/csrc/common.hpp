@@ -174,7 +174,12 @@ struct ScopedDevice {
 // Per-device scratch owned by the library: grown on demand, never shrunk,
 // released at process exit.  Used for split-K partials of the entry points
 // that have no workspace argument.
-void* device_workspace(int device, size_t bytes);
+// Slots: one cached buffer per (device, slot) so the decode partials and the
+// prefill V^T staging never share memory.
+constexpr int kWorkspaceDecode = 0;
+constexpr int kWorkspacePrefill = 1;
+constexpr int kWorkspaceSlots = 2;
+void* device_workspace(int device, size_t bytes, int slot);
 
 // Optional pair of events recorded on the launch stream immediately before and
 // after the dominant kernel of the next entry-point call (benchmarks time that

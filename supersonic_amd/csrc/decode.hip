@@ -584,7 +584,7 @@ static int run_decode(DecodeRequest& r) {
     if (ws) {
         if (r.workspace_bytes < need) return SUPERSONIC_ERR_WORKSPACE;
     } else {
-        ws = device_workspace(r.device, need);
+        ws = device_workspace(r.device, need, kWorkspaceDecode);
         if (!ws) return SUPERSONIC_ERR_WORKSPACE;
     }
     const size_t rows = static_cast<size_t>(r.B) * r.Hq * sp.nsplit;

@@ -8,21 +8,21 @@
 //   (split q/gate, QK RMSNorm, RoPE, transposes, cache copies, cast, gate).
 //
 // Kernel design (flash attention forward, fp32 accumulation):
-//   workgroup = 4 wave64s, 128 query rows of one head (32 rows per wave);
-//   keys in tiles of 64 staged through LDS: K row-major (16 B padded rows),
-//   V transposed (V^T[dim][token]) with a token permutation inside every
-//   16-token group so each MFMA operand fetch is one 16-byte ds_read.
-//   S^T = K Q^T   v_mfma_f32_32x32x16_{bf16,f16}: A = K rows, B = Q^T held in
-//                 registers for the whole kernel.  The C layout gives every
-//                 lane one query row and 16 keys of each 32-key block.
-//   O^T += V^T P^T: the B operand (P^T) is exactly the lane's own 8 softmax
-//                 weights per 16-key step: no shuffles between the two GEMMs.
-//   online softmax in base 2; one cross-lane max per tile (lane ^ 32).
-//   causal: key tiles past the workgroup's last row are never loaded; a wave
+//   workgroup = 128 query rows of one head: 8 compute wave64s of 16 rows and
+//   4 copy waves; keys in tiles of 64, double-buffered in LDS and copied
+//   global->LDS directly (buffer_load ... lds).  K is copied row-major into
+//   padded blocks; V comes from a transposed staging copy (vt_stage_kernel)
+//   so the PV operand is one conflict-free ds_read_b128 per MFMA.
+//   S^T = K Q^T     v_mfma_f32_16x16x32: A = 16 key rows (LDS), B = Q^T held
+//                   in registers for the whole kernel.
+//   O^T += V^T P^T  the B operand (P^T) is the lane's own softmax weights.
+//   Online softmax in base 2 with a lazy running max (O is rescaled only
+//   when a row max grows by more than 2^8); the row sums add the 16-bit
+//   weights exactly as the MFMA uses them.
+//   Causal: key tiles past the workgroup's last row are never loaded; a wave
 //   skips the MFMA work of tiles past its own last row; only tiles that cross
-//   the diagonal or the kv_len edge are masked.  Query tiles are scheduled
-//   longest first.
-//   Global -> register prefetch of the next K/V tile overlaps the MFMA work.
+//   the diagonal or the kv_len edge are masked.  Query tiles run longest
+//   first, the heads of one kv head on one XCD.
 #include <cstdlib>
 
 #include "common.hpp"
@@ -34,7 +34,11 @@ struct PrefillParams {
     const uint16_t* q;   // element (b, h, row, d) at b*q_bs + h*q_hs + row*q_rs + d
     int64_t q_bs, q_hs, q_rs;
     KvView kv;           // K/V rows of (b, kv head, token)
-    int Hq, G, S, L, off;
+    // V^T staging (vt_stage_kernel): element (b, kv head, dim, position) at
+    // ((b * Hkv + h) * D + dim) * vt_ld + position
+    const uint16_t* vt;
+    int vt_ld;
+    int Hq, Hkv, G, S, L, off;
     float scale_log2;
     int nqt;             // query tiles of 128 rows
     // drop-in output: f32, element (b, h, row, d) at b*o_bs + h*o_hs + row*o_rs + d
@@ -94,14 +98,59 @@ template <> __device__ __forceinline__ uint32_t cvt_pk<f16_t>(float a, float b) 
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// Tile geometry.  A K or V tile is 64 keys x D in LDS.  Copy instruction i
+// Sum of the two 16-bit weights packed in w, as the PV MFMA sees them (the
+// row sum then matches the weights in O exactly, so a dominant weight's
+// rounding cancels in O / l).
+template <typename QT> __device__ __forceinline__ float pk_sum(uint32_t w);
+template <> __device__ __forceinline__ float pk_sum<bf16_t>(uint32_t w) {
+    return __uint_as_float(w << 16) + __uint_as_float(w & 0xFFFF0000u);
+}
+template <> __device__ __forceinline__ float pk_sum<f16_t>(uint32_t w) {
+    const f16x2_v h = __builtin_bit_cast(f16x2_v, w);
+    return static_cast<float>(h[0]) + static_cast<float>(h[1]);
+}
+
+// Reductions over lanes l ^ 16 and l ^ 32 with the gfx950 permlane swaps
+// (VALU, no LDS round trip).  Each swap returns the lane's own value and its
+// partner's in some order, which is all a max or a sum needs.
+// max of three MFMA results as one v_max3_f32.  fmaxf would first quiet
+// every operand (a v_max_f32 x, x per value) because MFMA outputs are not
+// known to be canonical; scores are never signalling NaNs.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float xor16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return max3_raw(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return max3_raw(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Tile geometry.  A K tile is 64 keys x D in LDS.  Copy instruction i
 // (i < NR = D/8) of a tile moves rows i, i + NR, i + 2 NR, ... (64/NR rows,
-// one 1 KB run) into LDS block i.  Blocks are padded so reads hit distinct
-// banks: K and V blocks by 8 words each (measured on gfx950 with
-// SQ_LDS_BANK_CONFLICT over pads of 4/8/16/32 words: 8/8 is the only pair
-// without conflicts for the 16-row ds_read_b128 K reads and the 4-row
-// transposing V reads).  Row r lives at (r % NR) * BLK + (r / NR) *
-// ROWB, so every inner-loop LDS offset is an immediate on one per-lane base.
+// one 1 KB run) into LDS block i.  K blocks are padded by 8 words so the
+// 16-row ds_read_b128 K reads hit distinct banks (SQ_LDS_BANK_CONFLICT is 0
+// on gfx950).  Row r lives at (r % NR) * KBLK + (r / NR) * ROWB, so every
+// inner-loop LDS offset is an immediate on one per-lane base.
+//
+// A V tile arrives transposed: D rows (dims) of 64 keys, 128 B each, copy
+// instruction i moving dims 8i .. 8i + 7 into block i (1 KB, unpadded).  Dims
+// 16 P .. 16 P + 15 fill the 2 KB pair P; inside a pair dim r's 16-byte chunk
+// c (keys 8c .. 8c + 7 in staging order) sits at granule 8 r + (c ^ (r >> 1)),
+// which spreads the 16 dims one ds_read_b128 of the PV loop touches over all
+// 16 granule slots of a 256-byte bank row.
 template <int D> struct Tile {
     static constexpr int ROWB = 2 * D;        // bytes per key row
     static constexpr int NR = D / 8;          // copy instructions (= 1 KB blocks) per tile
@@ -115,17 +164,12 @@ template <int D> struct Tile {
 #ifndef SSA_KPAD
 #define SSA_KPAD 32
 #endif
-#ifndef SSA_VPAD
-#define SSA_VPAD 32
-#endif
     static constexpr int KBLK = 1024 + SSA_KPAD;
-    static constexpr int VBLK = 1024 + SSA_VPAD;
     static constexpr int KBYTES = NR * KBLK;
-    static constexpr int VBYTES = NR * VBLK;
+    static constexpr int VBYTES = NR * 1024;
     static constexpr int STAGE = KBYTES + VBYTES;
-    static constexpr int NI = NR / 8;         // copy instructions per wave (K and V each), 8 waves
+    static constexpr int NI = NR / 4;         // copy instructions per copy wave (K and V each)
     static __device__ __forceinline__ constexpr int koff(int r) { return (r % NR) * KBLK + (r / NR) * ROWB; }
-    static __device__ __forceinline__ constexpr int voff(int r) { return (r % NR) * VBLK + (r / NR) * ROWB; }
 };
 
 // Buffer resource for a tile base that is uniform across the wave (forced
@@ -153,11 +197,36 @@ template <> struct Mfma16<f16_t> {
     }
 };
 
-constexpr int kPrefillWaves = 8;   // 8 wave64s x 16 query rows = 128 rows per workgroup
+constexpr int kPrefillWaves = 8;   // compute waves: 8 x 16 query rows = 128 rows
+constexpr int kCopyWaves = 4;      // waves that only move K / V^T tiles into LDS
+constexpr int kPrefillThreads = 64 * (kPrefillWaves + kCopyWaves);
 
-// One workgroup = 128 query rows of one head; each wave owns 16 rows, so two
-// waves share a SIMD (about 200 registers each) and one wave's softmax VALU
-// work overlaps the other's MFMA chains.
+// Optional phase timeline (build with -DSSA_TRACE): wave 0 and wave 4 of the
+// first 16 workgroups stamp s_memtime at five points of each of their first
+// 64 key tiles; ssa_prefill_trace_dump copies the stamps out.
+#ifdef SSA_TRACE
+__device__ unsigned long long g_prefill_trace[16 * 2 * 64 * 5];
+#define SSA_STAMP(slot)                                                                                    \
+    do {                                                                                                   \
+        if (blockIdx.x < 16 && (wave & 3) == 0 && it < 64) {                                               \
+            __builtin_amdgcn_sched_barrier(0);                                                             \
+            const unsigned long long t_ = __builtin_amdgcn_s_memtime();                                    \
+            if (lane == 0) g_prefill_trace[((blockIdx.x * 2 + (wave >> 2)) * 64 + it) * 5 + (slot)] = t_; \
+            __builtin_amdgcn_sched_barrier(0);                                                             \
+        }                                                                                                  \
+    } while (0)
+#else
+#define SSA_STAMP(slot) \
+    do {                \
+    } while (0)
+#endif   // 8 wave64s x 16 query rows = 128 rows per workgroup
+
+// One workgroup = 128 query rows of one head: 8 compute waves of 16 rows each
+// plus 4 copy waves that only issue the global->LDS tile copies (the copy
+// path runs at about 48 B/clk per CU, and a wave that issues copies stalls
+// until they are accepted, so compute waves never issue any).  Three waves
+// share a SIMD (about 150 registers each); one wave's softmax VALU work
+// overlaps another's MFMA chains.
 //
 //   S^T = K Q^T      v_mfma_f32_16x16x32: A = 16 key rows (LDS), B = Q^T (16
 //                    query rows, registers).  C: lane l holds query row l & 15
@@ -167,7 +236,7 @@ constexpr int kPrefillWaves = 8;   // 8 wave64s x 16 query rows = 128 rows per w
 //                    operand (V^T) comes from two transposing LDS reads, each
 //                    giving a lane 4 consecutive keys of dim (l & 15).
 template <typename QT, int D, bool FUSED>
-__global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
     typedef typename Mfma16<QT>::op op_t;
     typedef Tile<D> T;
@@ -209,28 +278,50 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillPara
     const int lim_row = min(L, off + myrow + 1);
 
     // Direct global->LDS copy of key tile `it` into stage `st` (asynchronous,
-    // counted by vmcnt).  Lane l of copy instruction i moves 16 bytes of row
-    // i + NR (l / (D/8)); rows past kv_len fall outside the buffer range and
-    // read as zeros (masked later; never stale cache contents).
+    // counted by vmcnt).  K: lane l of copy instruction i moves 16 bytes of
+    // row i + NR (l / (D/8)); rows past kv_len fall outside the buffer range
+    // and read as zeros (masked later; never stale cache contents).  V^T:
+    // lane l of instruction i moves chunk c = (l & 7) ^ (4 (i & 1) + (l >> 4))
+    // of dim 8 i + (l >> 3) (the swizzle of the tile geometry); the staging
+    // buffer is zero past kv_len.
     const int dma_lane = (lane / (D / 8)) * T::NR * T::ROWB + (lane % (D / 8)) * 16;
+    const int vt_rowb = 2 * p.vt_ld;
+    const int vt_lane0 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (lane >> 4));
+    const int vt_lane1 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (4 + (lane >> 4)));
+    const uint16_t* vt_head = p.vt + (static_cast<int64_t>(b) * p.Hkv + kvh) * D * p.vt_ld;
     auto issue_tile = [&](int it, int st) {
         const int k0 = it * 64;
         const int64_t base = p.kv.row(b, kvh, k0, D) * 2;  // a tile lies inside one page
         const int bytes = min(64, L - k0) * T::ROWB;
         const __amdgpu_buffer_rsrc_t kr = tile_rsrc(p.kv.k + base, bytes);
-        const __amdgpu_buffer_rsrc_t vr = tile_rsrc(p.kv.v + base, bytes);
-        const int lbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + wave * T::NI * T::KBLK);
-        const int vbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + T::KBYTES + wave * T::NI * T::VBLK);
+        const __amdgpu_buffer_rsrc_t vr = tile_rsrc(reinterpret_cast<const uint8_t*>(vt_head + k0),
+                                                    D * vt_rowb - 2 * k0);
+        const int cw = wave - kPrefillWaves;
+        const int lbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + cw * T::NI * T::KBLK);
+        const int vbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + T::KBYTES + cw * T::NI * 1024);
 #pragma unroll
         for (int j = 0; j < T::NI; ++j) {
-            const int i = wave * T::NI + j;
+            const int i = cw * T::NI + j;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)(lds + lbase + j * T::KBLK),
                                                      16, dma_lane, i * T::ROWB, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(lds + vbase + j * T::VBLK),
-                                                     16, dma_lane, i * T::ROWB, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(lds + vbase + j * 1024),
+                                                     16, (i & 1) ? vt_lane1 : vt_lane0, 8 * i * vt_rowb, 0, 0);
         }
     };
-    if (ntiles > 0) issue_tile(0, 1);
+    if (wave >= kPrefillWaves) {
+        // Copy waves: tile it goes to stage (it + 1) & 1; the next tile is
+        // issued once everyone has passed the barrier of tile it (its stage's
+        // previous tile has been read).  Same barrier count as the compute
+        // waves; the stage-0 query staging of the fused prologue is finished
+        // before the first barrier.
+        if (ntiles > 0) issue_tile(0, 1);
+        for (int it = 0; it < ntiles; ++it) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (it + 1 < ntiles) issue_tile(it + 1, it & 1);
+        }
+        return;
+    }
 
     // ------------------------------------------------ Q^T operand (registers)
     // B operand of S^T = K Q^T: lane holds query row (lane & 15), dims 32 s + 8 g4 + j.
@@ -298,23 +389,26 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillPara
     float m_run = -1e30f, l_part = 0.f;
     const float c2 = p.scale_log2;
 
-    // Per-lane LDS bases: K row (lane & 15), dims 8 g4; V row (key) 4 g4 +
-    // ((lane & 15) >> 2), dims 4 (lane & 3).  For r < 16, koff(r + 16 m) -
-    // koff(r) and voff(r + 16 m) - voff(r) do not depend on r, so the other
-    // rows are the compile-time offsets koff(16 m), voff(16 m).
+    // Per-lane LDS bases: K row (lane & 15), dims 8 g4 (for r < 16,
+    // koff(r + 16 m) - koff(r) does not depend on r, so the other rows are the
+    // compile-time offsets koff(16 m)).  V^T: dim (lane & 15) of each pair,
+    // chunk 4 u + g4 of 32-key step u (swizzled granule).
     const int kbase_off = T::koff(lane & 15) + 16 * g4;
-    const int vbase_off = T::KBYTES + T::voff(4 * g4 + ((lane & 15) >> 2)) + 2 * 4 * (lane & 3);
+    const int vx = (lane & 15) >> 1;
+    const int vrd0 = T::KBYTES + 16 * (8 * (lane & 15) + (g4 ^ vx));
+    const int vrd1 = T::KBYTES + 16 * (8 * (lane & 15) + ((4 + g4) ^ vx));
 
     for (int it = 0; it < ntiles; ++it) {
         const int k0 = it * 64;
         const int st = (it + 1) & 1;
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile `it` have landed
-        __syncthreads();                // ... and everyone's; stage st^1 is free again
-        if (it + 1 < ntiles) issue_tile(it + 1, st ^ 1);
+        __syncthreads();                // the copy waves' tile `it` has landed; stage st^1 is free again
+        SSA_STAMP(0);
         if (k0 >= lim_wave) continue;   // the whole tile is past this wave's rows
+        SSA_STAMP(1);
 
         const uint8_t* kl = lds + st * T::STAGE + kbase_off;
-        const uint8_t* vl = lds + st * T::STAGE + vbase_off;
+        const uint8_t* vl0 = lds + st * T::STAGE + vrd0;
+        const uint8_t* vl1 = lds + st * T::STAGE + vrd1;
 
         // S^T = K Q^T, four 16-key blocks.
         f32x4_v sacc[4];
@@ -336,25 +430,32 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillPara
         }
         __builtin_amdgcn_sched_group_barrier(0x008, SSA_KLA, 0);
         __builtin_amdgcn_sched_barrier(0);
+        SSA_STAMP(2);
 
         // Online softmax, base 2, exact running max.  Lane holds row myrow and
         // keys k0 + 16 kb + 4 g4 + i.
         const bool need_mask = (k0 + 64 > off + row_w0 + 1) || (k0 + 64 > L);
-        float mx = -INFINITY;
+        if (need_mask) {
+            // Only tiles crossing the diagonal or kv_len: a real branch (the
+            // empty volatile asm keeps the compiler from if-converting it).
+            asm volatile("" ::: "memory");
+            const int rem = lim_row - (k0 + 4 * g4);  // key 16 kb + i is valid iff < rem
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+            for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float v = sacc[kb][i];
-                if (need_mask) {
-                    const int t = k0 + 16 * kb + 4 * g4 + i;
-                    if (t >= lim_row) v = -INFINITY;
-                }
-                sacc[kb][i] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32)) * c2;
+                for (int i = 0; i < 4; ++i)
+                    if (16 * kb + i >= rem) sacc[kb][i] = -INFINITY;
+        }
+        float mx = max3_raw(sacc[0][0], sacc[0][1], sacc[0][2]);
+        mx = max3_raw(mx, sacc[0][3], sacc[1][0]);
+        mx = max3_raw(mx, sacc[1][1], sacc[1][2]);
+        mx = max3_raw(mx, sacc[1][3], sacc[2][0]);
+        mx = max3_raw(mx, sacc[2][1], sacc[2][2]);
+        mx = max3_raw(mx, sacc[2][3], sacc[3][0]);
+        mx = max3_raw(mx, sacc[3][1], sacc[3][2]);
+        mx = max3_raw(mx, sacc[3][3], sacc[3][3]);
+        mx = xor16_max(mx);
+        mx = xor32_max(mx) * c2;
         if (__any(mx > m_run + p.rescale_slack)) {
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -377,43 +478,40 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillPara
                 for (int j = 0; j < 2; ++j) {
                     const float a = __builtin_amdgcn_exp2f(fmaf(sacc[2 * u + hb][2 * j], c2, -m_use));
                     const float c = __builtin_amdgcn_exp2f(fmaf(sacc[2 * u + hb][2 * j + 1], c2, -m_use));
-                    psum += a + c;
                     w[2 * hb + j] = cvt_pk<QT>(a, c);
+                    psum += pk_sum<QT>(w[2 * hb + j]);
                 }
             pk[u] = to_op<op_t>(w);
         }
         l_part += psum;
         __builtin_amdgcn_sched_barrier(0);
+        SSA_STAMP(3);
 
-        // O^T += V^T P^T: two 32-key steps; A operand rows (keys) 32 u + 4 g4
-        // + {0..3} and 32 u + 16 + 4 g4 + {0..3}, dim 16 d + (lane & 15).
+        // O^T += V^T P^T: two 32-key steps.  A operand: dims 16 d + (lane & 15),
+        // the 8 keys of staging chunk 4 u + g4, which are exactly the keys
+        // 32 u + 4 g4 + {0..3} and 32 u + 16 + 4 g4 + {0..3} that the lane's
+        // B operand (P^T) carries.
 #pragma unroll
-        for (int d = 0; d < DBK; ++d) {
+        for (int u = 0; u < 2; ++u) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const s16x4_v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(32 * u) + 32 * d));
-                const s16x4_v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4_v*)(vl + T::voff(32 * u + 16) + 32 * d));
-                const u32x2_v lw = __builtin_bit_cast(u32x2_v, lo);
-                const u32x2_v hw = __builtin_bit_cast(u32x2_v, hi);
-                const u32x4_v w = {lw[0], lw[1], hw[0], hw[1]};
-                oacc[d] = Mfma16<QT>::mma(to_op<op_t>(w), pk[u], oacc[d]);
+            for (int d = 0; d < DBK; ++d) {
+                const op_t va = to_op<op_t>(ld16((u ? vl1 : vl0) + 2048 * d));
+                oacc[d] = Mfma16<QT>::mma(va, pk[u], oacc[d]);
             }
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * SSA_VLA, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, SSA_VLA, 1);
 #pragma unroll
         for (int i = 0; i < 2 * DBK - SSA_VLA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, SSA_VLA, 1);
+        SSA_STAMP(4);
     }
 
     // ------------------------------------------------ epilogue
     // O^T C layout: lane holds row myrow, dims 16 d + 4 g4 + i.
-    float l_tot = l_part + __shfl_xor(l_part, 16);
-    l_tot += __shfl_xor(l_tot, 32);
+    const float l_tot = xor32_sum(xor16_sum(l_part));
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     if (!row_ok) return;
     if constexpr (!FUSED) {
@@ -433,13 +531,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(PrefillPara
             const u32x2_v gw = *reinterpret_cast<const u32x2_v*>(grow + dd);
             const float gv[4] = {bf16_bits_to_f32(gw[0] & 0xFFFFu), bf16_bits_to_f32(gw[0] >> 16),
                                  bf16_bits_to_f32(gw[1] & 0xFFFFu), bf16_bits_to_f32(gw[1] >> 16)};
-            uint32_t r[4];
+            float r[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float a = bf16_round(oacc[d][e] * inv);
-                r[e] = f32_to_bf16_bits(a * (1.0f / (1.0f + expf(-gv[e]))));
+                const uint32_t ab = cvt_pk<bf16_t>(oacc[d][e] * inv, 0.f);
+                const float a = bf16_bits_to_f32(ab & 0xFFFFu);
+                // sigmoid(g) = 1 / (1 + 2^(-g log2 e)), hardware exp2 and reciprocal
+                r[e] = a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv[e] * kLog2e));
             }
-            const u32x2_v o = {r[0] | (r[1] << 16), r[2] | (r[3] << 16)};
+            const u32x2_v o = {cvt_pk<bf16_t>(r[0], r[1]), cvt_pk<bf16_t>(r[2], r[3])};
             *reinterpret_cast<u32x2_v*>(orow + dd) = o;
         }
     }
@@ -582,14 +682,72 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(KvPrepParams p) {
 }
 
 // ----------------------------------------------------------------------------
+// V^T staging for the prefill kernel.  The PV product needs, per lane, 8
+// consecutive keys of one dim; the cache stores token rows.  This pass writes
+// each kv head's V transposed, dims as rows of vt_ld positions (kv_len rounded
+// up to 64, zero past kv_len), with the keys of every 32-key group stored in
+// the order the S^T accumulator hands them to the PV MFMA: position
+// 8 g + j holds key 4 g + j for j < 4 and key 16 + 4 g + (j - 4) for j >= 4.
+// One workgroup per (64-key tile, kv head, sequence).
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ constexpr int vt_key_of_position(int p) {
+    return (p & ~31) + ((p & 4) ? 16 : 0) + 4 * ((p & 31) >> 3) + (p & 3);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void vt_stage_kernel(KvView kv, uint16_t* vt, int Hkv, int L, int ld) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[64][D + 8];
+    const int t0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+    for (int idx = threadIdx.x; idx < 64 * (D / 8); idx += 256) {
+        const int r = idx / (D / 8), c = idx % (D / 8);
+        const int t = t0 + r;
+        u32x4_v w = {0u, 0u, 0u, 0u};
+        if (t < L) w = ld16(reinterpret_cast<const uint16_t*>(kv.v) + kv.row(b, h, t, D) + 8 * c);
+        *reinterpret_cast<u32x4_v*>(&tile[r][8 * c]) = w;
+    }
+    __syncthreads();
+    uint16_t* dst = vt + (static_cast<int64_t>(b) * Hkv + h) * D * ld + t0;
+    for (int idx = threadIdx.x; idx < D * 8; idx += 256) {
+        const int d = idx >> 3, c = idx & 7;
+        u32x4_v w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = static_cast<uint32_t>(tile[vt_key_of_position(8 * c + 2 * j)][d]) |
+                   (static_cast<uint32_t>(tile[vt_key_of_position(8 * c + 2 * j + 1)][d]) << 16);
+        st16(dst + static_cast<int64_t>(d) * ld + 8 * c, w);
+    }
+}
+
+// Stages V^T for `B` sequences of `L` keys into the prefill workspace slot of
+// `device` and points `p` at it.  Returns hipSuccess or the failing error.
+static hipError_t stage_vt(int device, hipStream_t st, const KvView& kv, int B, int Hkv, int L, int D,
+                           PrefillParams& p) {
+    const int ld = (L + 63) / 64 * 64;
+    const size_t bytes = static_cast<size_t>(B) * Hkv * D * ld * 2;
+    void* ws = device_workspace(device, bytes, kWorkspacePrefill);
+    if (!ws) return hipErrorOutOfMemory;
+    p.vt = static_cast<const uint16_t*>(ws);
+    p.vt_ld = ld;
+    const dim3 grid(ld / 64, Hkv, B);
+    uint16_t* vt = static_cast<uint16_t*>(ws);
+    switch (D) {
+    case 64: hipLaunchKernelGGL(vt_stage_kernel<64>, grid, dim3(256), 0, st, kv, vt, Hkv, L, ld); break;
+    case 128: hipLaunchKernelGGL(vt_stage_kernel<128>, grid, dim3(256), 0, st, kv, vt, Hkv, L, ld); break;
+    case 256: hipLaunchKernelGGL(vt_stage_kernel<256>, grid, dim3(256), 0, st, kv, vt, Hkv, L, ld); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------
 // Host side
 // ----------------------------------------------------------------------------
 template <typename QT, bool FUSED>
 static hipError_t launch_prefill(int D, dim3 grid, hipStream_t st, const PrefillParams& p) {
     switch (D) {
-    case 64: hipLaunchKernelGGL((prefill_kernel<QT, 64, FUSED>), grid, dim3(64 * kPrefillWaves), 0, st, p); break;
-    case 128: hipLaunchKernelGGL((prefill_kernel<QT, 128, FUSED>), grid, dim3(64 * kPrefillWaves), 0, st, p); break;
-    case 256: hipLaunchKernelGGL((prefill_kernel<QT, 256, FUSED>), grid, dim3(64 * kPrefillWaves), 0, st, p); break;
+    case 64: hipLaunchKernelGGL((prefill_kernel<QT, 64, FUSED>), grid, dim3(kPrefillThreads), 0, st, p); break;
+    case 128: hipLaunchKernelGGL((prefill_kernel<QT, 128, FUSED>), grid, dim3(kPrefillThreads), 0, st, p); break;
+    case 256: hipLaunchKernelGGL((prefill_kernel<QT, 256, FUSED>), grid, dim3(kPrefillThreads), 0, st, p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -597,7 +755,7 @@ static hipError_t launch_prefill(int D, dim3 grid, hipStream_t st, const Prefill
 
 static float rescale_slack() {
     const char* v = getenv("SUPERSONIC_PREFILL_RESCALE_SLACK");
-    return (v && *v) ? static_cast<float>(atof(v)) : 0.0f;
+    return (v && *v) ? static_cast<float>(atof(v)) : 8.0f;
 }
 
 static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t Hkv, size_t q_len, size_t kv_len,
@@ -630,6 +788,7 @@ static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t 
     p.kv.head_stride = static_cast<int64_t>(kv_len) * D;
     p.kv.seq_stride = static_cast<int64_t>(Hkv) * kv_len * D;
     p.Hq = static_cast<int>(Hq);
+    p.Hkv = static_cast<int>(Hkv);
     p.G = static_cast<int>(groups);
     p.S = static_cast<int>(q_len);
     p.L = static_cast<int>(kv_len);
@@ -642,6 +801,9 @@ static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t 
     p.o_hs = p.q_hs;
     p.o_bs = p.q_bs;
     dim3 grid(p.nqt * static_cast<unsigned>(Hq), static_cast<unsigned>(B));
+    if (kv_len > 0 && stage_vt(static_cast<int>(device), nullptr, p.kv, static_cast<int>(B), static_cast<int>(Hkv),
+                               static_cast<int>(kv_len), static_cast<int>(D), p) != hipSuccess)
+        return 11;
     const hipError_t e = dtype == 0 ? launch_prefill<f16_t, false>(static_cast<int>(D), grid, nullptr, p)
                                     : launch_prefill<bf16_t, false>(static_cast<int>(D), grid, nullptr, p);
     if (e != hipSuccess) return 11;
@@ -652,6 +814,12 @@ static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t 
 }  // namespace ssa
 
 using namespace ssa;
+
+#ifdef SSA_TRACE
+extern "C" int ssa_prefill_trace_dump(void* dst) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(ssa::g_prefill_trace), sizeof(ssa::g_prefill_trace)) == hipSuccess ? 0 : 1;
+}
+#endif
 
 extern "C" int supersonic_qwen35_hip_full_attention_prefill(
     int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads, size_t q_len,
@@ -712,6 +880,7 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.q_rs = static_cast<int64_t>(q_heads) * 2 * head_dim;
     p.kv = kv;
     p.Hq = static_cast<int>(q_heads);
+    p.Hkv = static_cast<int>(kv_heads);
     p.G = static_cast<int>(q_heads / kv_heads);
     p.S = static_cast<int>(chunk_len);
     p.L = static_cast<int>(chunk_start + chunk_len);
@@ -727,6 +896,8 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.half_rot = static_cast<int>(rotary_dim / 2);
     p.eps = eps;
     dim3 grid(p.nqt * static_cast<unsigned>(q_heads), 1);
+    if (stage_vt(static_cast<int>(device_ordinal), st, kv, 1, p.Hkv, p.L, static_cast<int>(head_dim), p) != hipSuccess)
+        return SUPERSONIC_ERR_LAUNCH;
     const ProfileEvents prof = take_profile_events();
     if (prof.before) (void)hipEventRecord(prof.before, st);
     if (launch_prefill<bf16_t, true>(static_cast<int>(head_dim), grid, st, p) != hipSuccess)

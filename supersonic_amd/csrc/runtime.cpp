@@ -12,17 +12,18 @@ struct Workspace {
     size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::vector<Workspace> g_ws;
+std::vector<Workspace> g_ws;  // index device * kWorkspaceSlots + slot
 }  // namespace
 
-// Returns a device buffer of at least `bytes` for `device`, growing the cached
-// one when needed.  The buffer is reused by every call on that device, so
-// calls that overlap on one device must pass their own workspace instead.
-void* device_workspace(int device, size_t bytes) {
+// Returns a device buffer of at least `bytes` for (`device`, `slot`), growing
+// the cached one when needed.  The buffer is reused by every call on that
+// device that uses the slot, so such calls that overlap on one device race.
+void* device_workspace(int device, size_t bytes, int slot) {
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    if (device < 0) return nullptr;
-    if (static_cast<size_t>(device) >= g_ws.size()) g_ws.resize(device + 1);
-    Workspace& w = g_ws[device];
+    if (device < 0 || slot < 0 || slot >= kWorkspaceSlots) return nullptr;
+    const size_t idx = static_cast<size_t>(device) * kWorkspaceSlots + slot;
+    if (idx >= g_ws.size()) g_ws.resize(idx + 1);
+    Workspace& w = g_ws[idx];
     if (w.bytes >= bytes && w.ptr) return w.ptr;
     if (w.ptr) {
         (void)hipDeviceSynchronize();
