@@ -98,17 +98,9 @@ template <> __device__ __forceinline__ uint32_t cvt_pk<f16_t>(float a, float b) 
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// Sum of the two 16-bit weights packed in w, as the PV MFMA sees them (the
-// row sum then matches the weights in O exactly, so a dominant weight's
-// rounding cancels in O / l).
-template <typename QT> __device__ __forceinline__ float pk_sum(uint32_t w);
-template <> __device__ __forceinline__ float pk_sum<bf16_t>(uint32_t w) {
-    return __uint_as_float(w << 16) + __uint_as_float(w & 0xFFFF0000u);
-}
-template <> __device__ __forceinline__ float pk_sum<f16_t>(uint32_t w) {
-    const f16x2_v h = __builtin_bit_cast(f16x2_v, w);
-    return static_cast<float>(h[0]) + static_cast<float>(h[1]);
-}
+// Two 16-bit ones packed in a word (the A operand of the row-sum MFMA).
+template <typename QT> constexpr uint32_t kOnePair = 0x3F803F80u;  // bf16 1.0, 1.0
+template <> constexpr uint32_t kOnePair<f16_t> = 0x3C003C00u;       // f16 1.0, 1.0
 
 // Reductions over lanes l ^ 16 and l ^ 32 with the gfx950 permlane swaps
 // (VALU, no LDS round trip).  Each swap returns the lane's own value and its
@@ -156,10 +148,10 @@ template <int D> struct Tile {
     static constexpr int NR = D / 8;          // copy instructions (= 1 KB blocks) per tile
 // LDS read lookahead of the K-operand (reads) and V-operand (MFMAs) pipelines
 #ifndef SSA_KLA
-#define SSA_KLA 6
+#define SSA_KLA 8
 #endif
 #ifndef SSA_VLA
-#define SSA_VLA 4
+#define SSA_VLA 6
 #endif
 #ifndef SSA_KPAD
 #define SSA_KPAD 32
@@ -205,13 +197,15 @@ constexpr int kPrefillThreads = 64 * (kPrefillWaves + kCopyWaves);
 // first 16 workgroups stamp s_memtime at five points of each of their first
 // 64 key tiles; ssa_prefill_trace_dump copies the stamps out.
 #ifdef SSA_TRACE
-__device__ unsigned long long g_prefill_trace[16 * 2 * 64 * 5];
+__device__ unsigned long long g_prefill_trace[16 * 2 * 64 * 6];
 #define SSA_STAMP(slot)                                                                                    \
     do {                                                                                                   \
         if (blockIdx.x < 16 && (wave & 3) == 0 && it < 64) {                                               \
             __builtin_amdgcn_sched_barrier(0);                                                             \
             const unsigned long long t_ = __builtin_amdgcn_s_memtime();                                    \
-            if (lane == 0) g_prefill_trace[((blockIdx.x * 2 + (wave >> 2)) * 64 + it) * 5 + (slot)] = t_; \
+            const unsigned long long r_ = (slot) == 0 ? __builtin_amdgcn_s_memrealtime() : 0ull;           \
+            if (lane == 0) g_prefill_trace[((blockIdx.x * 2 + (wave >> 2)) * 64 + it) * 6 + (slot)] = t_; \
+            if (lane == 0 && (slot) == 0) g_prefill_trace[((blockIdx.x * 2 + (wave >> 2)) * 64 + it) * 6 + 5] = r_; \
             __builtin_amdgcn_sched_barrier(0);                                                             \
         }                                                                                                  \
     } while (0)
@@ -386,7 +380,12 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     f32x4_v oacc[DBK];
 #pragma unroll
     for (int d = 0; d < DBK; ++d) oacc[d] = f32x4_v{0.f, 0.f, 0.f, 0.f};
-    float m_run = -1e30f, l_part = 0.f;
+    float m_run = -1e30f;
+    // Row sums on the MFMA pipe: lacc += ones * P^T sums each query's 16-bit
+    // weights exactly as the PV product uses them (every lane ends up with
+    // its own row's total in lacc[0]; the four entries are equal).
+    f32x4_v lacc = {0.f, 0.f, 0.f, 0.f};
+    const op_t ones = to_op<op_t>(u32x4_v{kOnePair<QT>, kOnePair<QT>, kOnePair<QT>, kOnePair<QT>});
     const float c2 = p.scale_log2;
 
     // Per-lane LDS bases: K row (lane & 15), dims 8 g4 (for r < 16,
@@ -460,14 +459,14 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
-            l_part *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lacc[i] *= alpha;
 #pragma unroll
             for (int d = 0; d < DBK; ++d)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) oacc[d][i] *= alpha;
         }
         const float m_use = m_run;
-        float psum = 0.f;
         op_t pk[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -479,11 +478,9 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                     const float a = __builtin_amdgcn_exp2f(fmaf(sacc[2 * u + hb][2 * j], c2, -m_use));
                     const float c = __builtin_amdgcn_exp2f(fmaf(sacc[2 * u + hb][2 * j + 1], c2, -m_use));
                     w[2 * hb + j] = cvt_pk<QT>(a, c);
-                    psum += pk_sum<QT>(w[2 * hb + j]);
                 }
             pk[u] = to_op<op_t>(w);
         }
-        l_part += psum;
         __builtin_amdgcn_sched_barrier(0);
         SSA_STAMP(3);
 
@@ -498,6 +495,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                 const op_t va = to_op<op_t>(ld16((u ? vl1 : vl0) + 2048 * d));
                 oacc[d] = Mfma16<QT>::mma(va, pk[u], oacc[d]);
             }
+            lacc = Mfma16<QT>::mma(ones, pk[u], lacc);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, SSA_VLA, 1);
 #pragma unroll
@@ -511,7 +509,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
 
     // ------------------------------------------------ epilogue
     // O^T C layout: lane holds row myrow, dims 16 d + 4 g4 + i.
-    const float l_tot = xor32_sum(xor16_sum(l_part));
+    const float l_tot = lacc[0];
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     if (!row_ok) return;
     if constexpr (!FUSED) {
