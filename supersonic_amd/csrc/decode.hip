@@ -10,10 +10,14 @@
 // Design (HBM-bound; every K/V byte is read exactly once):
 //   grid  = (split, kv_head, batch); a workgroup owns `chunk` consecutive tokens
 //           of one kv head and serves all G = Hq/Hkv query heads that share it.
-//   block = 4 wave64s; wave w takes the 16-token blocks w, w+4, ... of the chunk.
+//   block = 4 wave64s; wave w takes the 16-token blocks w, w+4, ... of the chunk,
+//           with the next block's K/V loads in flight (two register sets)
+//           while the current one is computed; two workgroups per CU.
+//   loads : buffer loads against a resource bound to the block's live rows
+//           (rows past kv_len read as zero), one per-lane offset per operand.
 //   QK^T  : v_mfma_f32_16x16x32_{bf16,f16}.  A = the G query heads (rows, zero
-//           padded to 16), B = 16 tokens of K loaded straight from HBM in the
-//           B-operand layout (16 B per lane per k-step).  The score tile lands
+//           padded to 16, kept in LDS), B = 16 tokens of K loaded straight from
+//           HBM in the B-operand layout (16 B per lane per k-step).  The score tile lands
 //           with one token per lane of each 16-lane DPP row, so softmax row
 //           statistics are 4 DPP row_ror steps.
 //   softmax: online, base 2, per head; per-lane partial sums reduced once.
@@ -25,8 +29,9 @@
 //           K scale multiplies the score, the V scale multiplies p.
 //   Fused prologue: the workgroup normalises + rotates its q heads; the split
 //           that owns the new token also normalises + rotates k, writes K/V
-//           (or fp8 codes + scales) into the cache and reads the new token from
-//           LDS, unquantised (as full_attention_4b.hip:5351-5353 does).
+//           (or fp8 codes + scales) into the cache and, after its cached
+//           blocks, processes the new token as a one-token block read from LDS,
+//           unquantised (as full_attention_4b.hip:5351-5353 does).
 #include <cstdlib>
 #include <mutex>
 #include <utility>
@@ -105,13 +110,24 @@ __device__ __forceinline__ void fp8x8_to_f32(u32x2_v w, float* f) {
     }
 }
 
+// Buffer resource for a base that is uniform across the wave (forced into
+// SGPRs: it can come from a block-table load the compiler cannot prove
+// uniform).  Reads at or past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const uint8_t* base, int bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+    void* u = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, static_cast<short>(0), bytes, 0x00020000);
+}
+
 template <typename QT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);
 }
 
 template <typename QT, bool FP8, int D, int GP>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(DecodeParams p) {
     static_assert(D % 64 == 0 && D <= 512, "head_dim");
     static_assert(GP == 4 || GP == 8 || GP == 16, "padded group");
     typedef typename Mfma<QT>::op op_t;
@@ -211,8 +227,10 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
     }
 
     // Q as the MFMA A operand: row = head (lane & 15), k = dims 32s + 8(lane>>4) + j.
-    op_t qa[KSTEPS];
-    {
+    // Kept in LDS (one copy for the 4 waves) and read back per block, which
+    // leaves registers for the next block's loads.
+    __shared__ u32x4_v qop_s[KSTEPS * 64];
+    if (wave == 0) {
         const int hh = lane & 15;
         const int dk = 8 * (lane >> 4);
 #pragma unroll
@@ -227,7 +245,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
                 }
                 w[j] = pack2<QT>(a, c);
             }
-            qa[s] = as_op<op_t>(w);
+            qop_s[s * 64 + lane] = w;
         }
     }
     __syncthreads();  // smem is reused by the merge below
@@ -245,73 +263,73 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
     const int n_s = lane & 15;           // score lane: token within the block
     const int vt = lane / LPT;           // V lane: token within the instruction
     const int vd = (lane % LPT) * 8;     // V lane: first dim
-    const int nblk = (t_end - t_begin + 15) >> 4;
+    // Cached tokens of this split; the owner's new token (the last one) is
+    // handled after the loop.
+    const int t_main = owner ? pos : t_end;
+    const int nblk = (t_main - t_begin + 15) >> 4;
     const uint8_t* kbase = p.kv.k;
     const uint8_t* vbase = p.kv.v;
 
-    for (int blk = wave; blk < nblk; blk += 4) {
-        const int t0 = t_begin + blk * 16;
-        const int64_t base = p.kv.row(b, kvh, t0, D);  // block lies inside one page
-        const int last = len - 1 - t0;                  // clamp loads to live rows
-
-        // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
+    // Block data of one 16-token block, loaded one block ahead (registers).
+    struct Blk {
         op_t kb[KSTEPS];
-        {
-            const int kn = min(n_s, last);
-            const uint8_t* kp = kbase + (base + static_cast<int64_t>(kn) * D + 8 * (lane >> 4)) * ESZ;
+        u32x4_v vr16[FP8 ? 1 : VINS];
+        u32x2_v vr8[FP8 ? VINS : 1];
+        float ksc, vsc;
+    };
+    // Buffer resources bound to the block's live rows (a block lies inside one
+    // page): rows past kv_len read as zeros, so every load is one per-lane
+    // offset plus a constant, with no per-load clamping.
+    const int k_lane_off = (n_s * D + 8 * (lane >> 4)) * ESZ;
+    const int v_lane_off = (vt * D + vd) * ESZ;
+    auto fetch = [&](int blk, Blk& B) {
+        const int t0 = t_begin + blk * 16;
+        const int64_t base = p.kv.row(b, kvh, t0, D);
+        const int nvalid = min(16, t_main - t0);
+        const __amdgpu_buffer_rsrc_t kr = uniform_rsrc(kbase + base * ESZ, nvalid * D * ESZ);
+        const __amdgpu_buffer_rsrc_t vr = uniform_rsrc(vbase + base * ESZ, nvalid * D * ESZ);
+        // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
 #pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) {
-                if constexpr (!FP8) {
-                    kb[s] = as_op<op_t>(ld16(kp + 64 * s));
-                } else {
-                    kb[s] = as_op<op_t>(fp8x8_to_bf16x8(*reinterpret_cast<const u32x2_v*>(kp + 32 * s)));
-                }
+        for (int s = 0; s < KSTEPS; ++s) {
+            if constexpr (!FP8) {
+                B.kb[s] = as_op<op_t>(__builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * s, 0, 0)));
+            } else {
+                B.kb[s] = as_op<op_t>(fp8x8_to_bf16x8(__builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane_off + 32 * s, 0, 0))));
             }
         }
         // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
-        u32x4_v vr16[FP8 ? 1 : VINS];
-        u32x2_v vr8[FP8 ? VINS : 1];
 #pragma unroll
         for (int j = 0; j < VINS; ++j) {
-            const int tk = min(TPI * j + vt, last);
-            const uint8_t* vp = vbase + (base + static_cast<int64_t>(tk) * D + vd) * ESZ;
-            if constexpr (!FP8) vr16[j] = ld16(vp);
-            else vr8[j] = *reinterpret_cast<const u32x2_v*>(vp);
+            const int jo = TPI * j * D * ESZ;
+            if constexpr (!FP8) B.vr16[j] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane_off, jo, 0));
+            else B.vr8[j] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane_off, jo, 0));
         }
-        float ksc = 1.f, vsc = 1.f;
+        B.ksc = 1.f;
+        B.vsc = 1.f;
         if constexpr (FP8) {
             const int64_t sb = p.kv.srow(b, kvh, t0);
-            const int kn = min(n_s, last);
-            ksc = p.kv.ks[sb + kn];
-            vsc = p.kv.vs[sb + kn];
+            const int kn = min(n_s, nvalid - 1);
+            B.ksc = p.kv.ks[sb + kn];
+            B.vsc = p.kv.vs[sb + kn];
         }
-        const bool has_new = owner && pos >= t0 && pos < t0 + 16;
-        if (has_new && n_s == pos - t0) {
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) {
-                u32x4_v w;
-                const int d0 = 32 * s + 8 * (lane >> 4);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(kn_s[d0 + 2 * j], kn_s[d0 + 2 * j + 1]);
-                kb[s] = as_op<op_t>(w);
-            }
-            ksc = 1.f;
-            vsc = 1.f;
-        }
-
+    };
+    // One 16-token block: scores on the MFMA pipe, online softmax per head,
+    // PV on VALU.  Tokens n_s >= nv are masked.  vdec(j, vf) yields the 8
+    // dims of V row TPI*j + vt as floats.
+    auto process = [&](int nv, const op_t (&kb)[KSTEPS], float ksc, float vsc, auto&& vdec) {
         f32x4_v sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) sc = Mfma<QT>::mma(qa[s], kb[s], sc);
+        for (int s = 0; s < KSTEPS; ++s) sc = Mfma<QT>::mma(as_op<op_t>(qop_s[s * 64 + lane]), kb[s], sc);
 
-        const bool valid = (t0 + n_s) < t_end;
+        const bool valid = n_s < nv;
         float pr[4], al[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float s2 = valid ? sc[i] * (p.scale_log2 * ksc) : -INFINITY;
             const float bm = row16_max(s2);
             const float mn = fmaxf(m[i], bm);
-            al[i] = exp2f(m[i] - mn);
-            const float pe = exp2f(s2 - mn);
+            al[i] = __builtin_amdgcn_exp2f(m[i] - mn);
+            const float pe = __builtin_amdgcn_exp2f(s2 - mn);
             lsum[i] = lsum[i] * al[i] + pe;
             m[i] = mn;
             pr[i] = pe * vsc;
@@ -337,12 +355,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
         for (int j = 0; j < VINS; ++j) {
             const int tn = TPI * j + vt;
             float vf[8];
-            if constexpr (!FP8) unpack8<QT>(vr16[j], vf);
-            else fp8x8_to_f32(vr8[j], vf);
-            if (has_new && tn == pos - t0) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) vf[e] = vn_s[vd + e];
-            }
+            vdec(j, vf);
             float pv[GP];
 #pragma unroll
             for (int h4 = 0; h4 < GP / 4; ++h4) {
@@ -359,6 +372,45 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
+    };
+    auto process_blk = [&](int blk, Blk& B) {
+        const int t0 = t_begin + blk * 16;
+        process(min(16, t_main - t0), B.kb, B.ksc, B.vsc, [&](int j, float (&vf)[8]) {
+            if constexpr (!FP8) unpack8<QT>(B.vr16[j], vf);
+            else fp8x8_to_f32(B.vr8[j], vf);
+        });
+    };
+
+    // Software pipeline: the next block's loads are in flight while the
+    // current block is computed (two register sets, unrolled by two).
+    {
+        Blk A, Bn;
+        if (wave < nblk) fetch(wave, A);
+        for (int blk = wave; blk < nblk; blk += 8) {
+            if (blk + 4 < nblk) fetch(blk + 4, Bn);
+            process_blk(blk, A);
+            if (blk + 4 >= nblk) break;
+            if (blk + 8 < nblk) fetch(blk + 8, A);
+            process_blk(blk + 4, Bn);
+        }
+    }
+    // The new token (fused owner split): one more block of one token, read
+    // from LDS unquantised (as full_attention_4b.hip:5351-5353 does), on wave 0.
+    if (owner && wave == 0) {
+        op_t kbn[KSTEPS];
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            u32x4_v w;
+            const int d0 = 32 * s + 8 * (lane >> 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(kn_s[d0 + 2 * j], kn_s[d0 + 2 * j + 1]);
+            kbn[s] = as_op<op_t>(w);
+        }
+        process(1, kbn, 1.f, 1.f, [&](int j, float (&vf)[8]) {
+            const bool mine = TPI * j + vt == 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vf[e] = mine ? vn_s[vd + e] : 0.f;
+        });
     }
 
     // ---------------------------------------------------------------- merge
@@ -509,7 +561,7 @@ static int env_int(const char* name, int dflt) {
 // Chunk of tokens per workgroup: enough workgroups to fill 256 CUs a few
 // times over, but chunks of at least 64 tokens (4 waves x 16).
 static SplitPlan plan_splits(int B, int Hkv, int max_len) {
-    const int target = env_int("SUPERSONIC_DECODE_TARGET_WGS", 1024);
+    const int target = env_int("SUPERSONIC_DECODE_TARGET_WGS", 512);
     const int min_chunk = env_int("SUPERSONIC_DECODE_MIN_CHUNK", 128);
     const int pairs = B * Hkv;
     int want = (target + pairs - 1) / pairs;
