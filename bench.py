@@ -178,7 +178,7 @@ class Workloads:
             else:
                 caches.append(K.KvCache(kk, vv, block_table=bt))
         out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=self.dev)
-        ws = torch.empty(K.decode_workspace_size(B, Hq, Hkv, D, max(lens) + 1), dtype=torch.uint8, device=self.dev)
+        ws = torch.zeros(K.decode_workspace_size(B, Hq, Hkv, D, max(lens) + 1), dtype=torch.uint8, device=self.dev)
         args = dict(q_proj=q_proj, k_new=k_new, v_new=v_new, qw=qw, kw=kw, cos=cos.to(self.dev),
                     sin=sin.to(self.dev), pos=pos, out=out, ws=ws)
 

@@ -23,8 +23,9 @@
 //   softmax: online, base 2, per head; per-lane partial sums reduced once.
 //   PV    : VALU; each lane owns 8 dims of one token (128-bit loads), P is
 //           broadcast through a per-wave LDS tile.
-//   merge : the 4 waves merge through LDS; splits merge in a second kernel
-//           (log-sum-exp), which also applies the sigmoid gate.
+//   merge : the 4 waves merge through LDS; the last split of each (b, kv head)
+//           to arrive (device-scope counter) merges the splits (log-sum-exp)
+//           and applies the sigmoid gate, so one kernel does the whole step.
 //   FP8   : e4m3 bytes -> bf16 with the hardware OCP converter; the per-token
 //           K scale multiplies the score, the V scale multiplies p.
 //   Fused prologue: the workgroup normalises + rotates its q heads; the split
@@ -62,6 +63,10 @@ struct DecodeParams {
     float eps;
     float* part_o;            // [B, Hq, nsplit, D]
     float* part_ml;           // [B, Hq, nsplit, 2] (max in log2 units, sum)
+    unsigned* arrivals;       // [B, Hkv] split arrival counters, zero between calls
+    const uint16_t* gate;     // NULL, or gate element (b, h, d) at b*g_bstride + h*g_hstride + d
+    int64_t g_bstride, g_hstride;
+    void* out;                // [B, Hq*D] of QT
 };
 
 template <typename QT> struct Mfma;
@@ -121,6 +126,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const uint8_t* ba
     return __builtin_amdgcn_make_buffer_rsrc(u, static_cast<short>(0), bytes, 0x00020000);
 }
 
+// Device-coherent (sc1) relaxed accesses: visible across the XCDs' L2s without
+// a device-wide fence.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename QT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);
@@ -146,7 +160,16 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int len = p.lens[b] + p.len_plus;
     const int t_begin = split * p.chunk;
-    if (t_begin >= len) return;  // uniform: ragged batch, nothing to do
+    if (t_begin >= len) {  // uniform: ragged batch, nothing to do
+        if (len <= 0 && split == 0) {
+            // No tokens at all: the output is zero (what the merge of no splits gives).
+            for (int idx = tid; idx < p.G * D; idx += 256) {
+                const int h = kvh * p.G + idx / D;
+                store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + idx % D, 0.f);
+            }
+        }
+        return;
+    }
     const int t_end = min(len, t_begin + p.chunk);
     const int G = p.G;
     const int pos = len - 1;
@@ -313,6 +336,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
             B.vsc = p.kv.vs[sb + kn];
         }
     };
+
     // One 16-token block: scores on the MFMA pipe, online softmax per head,
     // PV on VALU.  Tokens n_s >= nv are masked.  vdec(j, vf) yields the 8
     // dims of V row TPI*j + vt as floats.
@@ -478,9 +502,8 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
                     for (int e = 0; e < 8; ++e) o[e] = acc[h][e] + smem[h * D + vd + e];
                     const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
                     float* dst = p.part_o + row * D + vd;
-                    f32x4_v o0 = {o[0], o[1], o[2], o[3]}, o1 = {o[4], o[5], o[6], o[7]};
-                    *reinterpret_cast<f32x4_v*>(dst) = o0;
-                    *reinterpret_cast<f32x4_v*>(dst + 4) = o1;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) store_agent(dst + e, o[e]);
                 }
             }
         }
@@ -493,55 +516,78 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
 #pragma unroll
             for (int w = 0; w < 4; ++w) L += exp2f(ml_s[w][h][0] - M) * ml_s[w][h][1];
             const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
-            p.part_ml[2 * row] = M;
-            p.part_ml[2 * row + 1] = L;
+            store_agent(&p.part_ml[2 * row], M);
+            store_agent(&p.part_ml[2 * row + 1], L);
         }
     }
-}
 
-// ----------------------------------------------------------------------------
-// Split merge + output cast + optional sigmoid gate.
-// grid = (Hq, B, D/64), block = 64.
-// ----------------------------------------------------------------------------
-struct MergeParams {
-    const float* part_o;
-    const float* part_ml;
-    const int32_t* lens;
-    int len_plus;
-    int Hq, D, chunk, nsplit;
-    const uint16_t* gate;     // NULL, or gate element (b, h, d) at b*g_bstride + h*g_hstride + d
-    int64_t g_bstride, g_hstride;
-    void* out;                // [B, Hq*D] of OT
-};
-
-template <typename OT>
-__global__ __launch_bounds__(64) void decode_merge_kernel(MergeParams p) {
-    __shared__ float f_s[1024];
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int d = blockIdx.z * 64 + threadIdx.x;
-    const int len = p.lens[b] + p.len_plus;
-    const int ns = len > 0 ? (len + p.chunk - 1) / p.chunk : 0;
-    const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + h) * p.nsplit;
-    float M = -1e30f;
-    for (int s = threadIdx.x; s < ns; s += 64) M = fmaxf(M, p.part_ml[2 * (row0 + s)]);
-    M = wave_max(M);
-    float L = 0.f;
-    for (int s = threadIdx.x; s < ns; s += 64) {
-        const float f = exp2f(p.part_ml[2 * (row0 + s)] - M);
-        f_s[s] = f;
-        L += f * p.part_ml[2 * (row0 + s) + 1];
-    }
-    L = wave_sum(L);
+    // ---------------------------------------------------------------- split merge
+    // The last split of (b, kv head) to arrive merges all of them (log-sum-exp)
+    // and applies the gate.  The partials are written and read with device-
+    // coherent (sc1) accesses, and the writer waits for its stores to complete
+    // before it arrives, so no device-wide fence (an L2 writeback and
+    // invalidate on this GPU) is needed.
+    __shared__ int last_s;
+    const int ns = (len + p.chunk - 1) / p.chunk;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
     __syncthreads();
-    float o = 0.f;
-    for (int s = 0; s < ns; ++s) o = fmaf(f_s[s], p.part_o[(row0 + s) * p.D + d], o);
-    float r = L > 0.f ? o / L : 0.f;
-    const int64_t oi = (static_cast<int64_t>(b) * p.Hq + h) * p.D + d;
-    if (p.gate) {
-        const float g = bf16_bits_to_f32(p.gate[b * p.g_bstride + h * p.g_hstride + d]);
-        r = bf16_round(bf16_round(r) * (1.0f / (1.0f + expf(-g))));
+    if (tid == 0) {
+        const unsigned prev = atomicAdd(&p.arrivals[b * p.Hkv + kvh], 1u);
+        last_s = prev == static_cast<unsigned>(ns - 1);
     }
-    store_f32(static_cast<OT*>(p.out), oi, r);
+    __syncthreads();
+    if (!last_s) return;
+    for (int hh = wave; hh < G; hh += 4) {
+        const int h = kvh * G + hh;
+        const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + h) * p.nsplit;
+        // One online pass over the splits, MCH at a time with all their loads
+        // in flight together (a handful of round trips instead of one per split).
+        constexpr int DPL = D / 64;  // dims per lane
+        constexpr int MCH = 16;
+        float M = -1e30f, Ls = 0.f, o[DPL];
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) o[k] = 0.f;
+        for (int s0 = 0; s0 < ns; s0 += MCH) {
+            float ms[MCH], ls[MCH], os[MCH][DPL];
+#pragma unroll
+            for (int c = 0; c < MCH; ++c) {
+                const int sc = min(s0 + c, ns - 1);  // duplicates past ns get zero weight below
+                ms[c] = load_agent(&p.part_ml[2 * (row0 + sc)]);
+                ls[c] = load_agent(&p.part_ml[2 * (row0 + sc) + 1]);
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) os[c][k] = load_agent(&p.part_o[(row0 + sc) * D + lane + 64 * k]);
+            }
+            float mc = M;
+#pragma unroll
+            for (int c = 0; c < MCH; ++c)
+                if (s0 + c < ns) mc = fmaxf(mc, ms[c]);
+            const float a = __builtin_amdgcn_exp2f(M - mc);
+            Ls *= a;
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) o[k] *= a;
+#pragma unroll
+            for (int c = 0; c < MCH; ++c) {
+                const float f = s0 + c < ns ? __builtin_amdgcn_exp2f(ms[c] - mc) : 0.f;
+                Ls = fmaf(f, ls[c], Ls);
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) o[k] = fmaf(f, os[c][k], o[k]);
+            }
+            M = mc;
+        }
+        const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+            const int d = lane + 64 * k;
+            float r = o[k] * inv;
+            if (p.gate) {
+                // bf16(bf16(attn) * sigmoid(gate)) (full_attention_4b.hip:5464-5470)
+                const float g = bf16_bits_to_f32(p.gate[b * p.g_bstride + h * p.g_hstride + d]);
+                r = bf16_round(bf16_round(r) * (1.0f / (1.0f + expf(-g))));
+            }
+            store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + d, r);
+        }
+    }
+    if (tid == 0) p.arrivals[b * p.Hkv + kvh] = 0u;  // every split has arrived: ready for the next call
 }
 
 // ----------------------------------------------------------------------------
@@ -580,9 +626,16 @@ static SplitPlan plan_splits(int B, int Hkv, int max_len) {
 
 static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+// Workspace: [arrival counters, kArrivalBytes][part_o][part_ml].  The
+// counters sit at a fixed offset so they never overlap partials of a call
+// with another shape; they are zero before the first call (a fresh library
+// workspace is zero-filled) and every call leaves them zero.
+constexpr size_t kArrivalBytes = 64 * 1024;
+constexpr int kMaxArrivals = static_cast<int>(kArrivalBytes / sizeof(unsigned));
+
 static size_t workspace_bytes_for(int B, int Hq, int D, int nsplit) {
     const size_t rows = static_cast<size_t>(B) * Hq * nsplit;
-    return align256(rows * D * sizeof(float)) + align256(rows * 2 * sizeof(float));
+    return kArrivalBytes + align256(rows * D * sizeof(float)) + align256(rows * 2 * sizeof(float));
 }
 
 template <typename QT, bool FP8, int D>
@@ -629,6 +682,7 @@ static int run_decode(DecodeRequest& r) {
     if (G > 16) return SUPERSONIC_ERR_HEADS;
     const int GP = G <= 4 ? 4 : (G <= 8 ? 8 : 16);
     if (r.B <= 0) return 0;
+    if (static_cast<int64_t>(r.B) * r.Hkv > kMaxArrivals) return SUPERSONIC_ERR_RANGE;
     if (r.max_len <= 0) r.max_len = 1;
     const SplitPlan sp = plan_splits(r.B, r.Hkv, r.max_len);
     const size_t need = workspace_bytes_for(r.B, r.Hq, r.D, sp.nsplit);
@@ -647,8 +701,13 @@ static int run_decode(DecodeRequest& r) {
     p.chunk = sp.chunk;
     p.nsplit = sp.nsplit;
     p.scale_log2 = r.scale * kLog2e;
-    p.part_o = static_cast<float*>(ws);
-    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(rows * r.D * sizeof(float)));
+    p.arrivals = static_cast<unsigned*>(ws);
+    p.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes);
+    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes + align256(rows * r.D * sizeof(float)));
+    p.gate = r.gate;
+    p.g_bstride = r.g_bstride;
+    p.g_hstride = r.g_hstride;
+    p.out = r.out;
 
     dim3 grid(sp.nsplit, r.Hkv, r.B);
     const ProfileEvents prof = take_profile_events();
@@ -660,23 +719,6 @@ static int run_decode(DecodeRequest& r) {
     if (e != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
     if (prof.after) (void)hipEventRecord(prof.after, r.stream);
 
-    MergeParams mp;
-    mp.part_o = p.part_o;
-    mp.part_ml = p.part_ml;
-    mp.lens = p.lens;
-    mp.len_plus = p.len_plus;
-    mp.Hq = r.Hq;
-    mp.D = r.D;
-    mp.chunk = sp.chunk;
-    mp.nsplit = sp.nsplit;
-    mp.gate = r.gate;
-    mp.g_bstride = r.g_bstride;
-    mp.g_hstride = r.g_hstride;
-    mp.out = r.out;
-    dim3 mg(r.Hq, r.B, r.D / 64);
-    if (r.qdtype == 0) hipLaunchKernelGGL(decode_merge_kernel<f16_t>, mg, dim3(64), 0, r.stream, mp);
-    else hipLaunchKernelGGL(decode_merge_kernel<bf16_t>, mg, dim3(64), 0, r.stream, mp);
-    if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
     return 0;
 }
 
@@ -745,9 +787,7 @@ static int decode_flat_common(int dtype, size_t device, size_t B, size_t Hq, siz
     p.lens = lens;
     p.len_plus = 0;
     p.fused = 0;
-    if (kv_len == 0) {
-        // every row is empty: the merge writes zeros
-    }
+    // kv_len == 0: split 0 of every (b, kv head) writes zeros.
     const int rc = run_decode(r);
     if (rc == SUPERSONIC_ERR_LAUNCH || rc == SUPERSONIC_ERR_WORKSPACE) return 402;
     if (rc != 0) return 401;

@@ -36,6 +36,13 @@ void* device_workspace(int device, size_t bytes, int slot) {
         w.ptr = nullptr;
         return nullptr;
     }
+    // Zero-filled once: kernels that keep counters in the workspace rely on
+    // it and leave them zero after every call.
+    if (hipMemset(w.ptr, 0, want) != hipSuccess) {
+        (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+        return nullptr;
+    }
     w.bytes = want;
     return w.ptr;
 }

@@ -155,6 +155,22 @@ def test_fused_decode_bf16(B, Hq, Hkv, D, rot, lens):
         assert torch.equal(cache.k[b, :, :p].cpu(), case["k"][b, :, :p])
 
 
+def test_fused_decode_caller_workspace_reuse():
+    """A zero-filled caller workspace serves consecutive calls of different
+    shapes (the split counters in its first 64 KiB are left at zero)."""
+    announce("fused decode caller workspace reuse")
+    n = max(K.decode_workspace_size(4, 16, 4, 256, 4097), K.decode_workspace_size(2, 8, 2, 128, 2049))
+    ws = torch.zeros(n, dtype=torch.uint8, device=DEV)
+    for seed, (B, Hq, Hkv, D, lens) in enumerate([(4, 16, 4, 256, [4096, 10, 2000, 777]),
+                                                   (2, 8, 2, 128, [2048, 5]),
+                                                   (4, 16, 4, 256, [100, 4096, 3, 64])]):
+        case = make_decode_case(40 + seed, B, Hq, Hkv, D, 64 if D == 256 else 32, lens)
+        out, _ = run_fused(case, workspace=ws)
+        ref, _, _, _, _ = oracle_decode(case)
+        check(out, ref, TOL_BF16, f"workspace reuse {seed}")
+        assert int(ws[:65536].count_nonzero()) == 0
+
+
 @pytest.mark.parametrize("B,lens", [(4, [1024, 16383, 5000, 77]), (2, [0, 33])])
 def test_fused_decode_fp8(B, lens):
     announce(f"fused decode fp8 lens={lens}")
