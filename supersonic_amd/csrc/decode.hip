@@ -140,8 +140,29 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);
 }
 
+// Optional timeline (build with -DSSA_TRACE): thread 0 of each of the first
+// 4096 workgroups stamps s_memrealtime at kernel entry, loop start, loop end,
+// after the partials, and exit; ssa_decode_trace_dump copies them out.
+#ifdef SSA_TRACE
+__device__ unsigned long long g_decode_trace[4096 * 6];
+#define SSA_DSTAMP(slot)                                                                                   \
+    do {                                                                                                   \
+        const unsigned wg_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);               \
+        if (tid == 0 && wg_ < 4096) g_decode_trace[wg_ * 6 + (slot)] = __builtin_amdgcn_s_memrealtime();   \
+    } while (0)
+#else
+#define SSA_DSTAMP(slot) \
+    do {                 \
+    } while (0)
+#endif
+
+// Waves per workgroup: 8 for head groups up to 4 (one workgroup per CU, two
+// waves per SIMD at up to 256 registers); the larger groups need more
+// registers and run 4 (two workgroups per CU for 8, one for 16).
+__host__ __device__ constexpr int decode_waves(int GP) { return GP <= 4 ? 8 : 4; }
+
 template <typename QT, bool FP8, int D, int GP>
-__global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(DecodeParams p) {
     static_assert(D % 64 == 0 && D <= 512, "head_dim");
     static_assert(GP == 4 || GP == 8 || GP == 16, "padded group");
     typedef typename Mfma<QT>::op op_t;
@@ -151,10 +172,13 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     constexpr int VINS = 16 / TPI;   // V load instructions per 16-token block
     constexpr int ESZ = FP8 ? 1 : 2;
 
-    __shared__ float smem[2 * GP * D];         // q staging, then the wave merge
-    __shared__ float p_s[4][16][GP];           // per-wave probabilities
+    constexpr int NW = decode_waves(GP);
+    constexpr int NT = 64 * NW;
+    __shared__ float smem[(NW / 2 > 2 ? NW / 2 : 2) * GP * D];  // q staging, then the wave merge
+    __shared__ float p_s[NW][16][GP];          // per-wave probabilities
     __shared__ float kn_s[D], vn_s[D];         // the new token (fused owner split)
-    __shared__ float ml_s[4][GP][2];
+    __shared__ float ml_s[NW][GP][2];
+    __shared__ int next_blk;                   // next 16-token block to claim
 
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -163,7 +187,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     if (t_begin >= len) {  // uniform: ragged batch, nothing to do
         if (len <= 0 && split == 0) {
             // No tokens at all: the output is zero (what the merge of no splits gives).
-            for (int idx = tid; idx < p.G * D; idx += 256) {
+            for (int idx = tid; idx < p.G * D; idx += NT) {
                 const int h = kvh * p.G + idx / D;
                 store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + idx % D, 0.f);
             }
@@ -174,16 +198,18 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     const int G = p.G;
     const int pos = len - 1;
     const bool owner = p.fused && pos >= t_begin && pos < t_end;
+    SSA_DSTAMP(0);
 
     // ---------------------------------------------------------------- prologue
-    for (int idx = tid; idx < GP * D; idx += 256) {
+    if (tid == 0) next_blk = NW;  // blocks 0 .. NW-1 are the waves' first
+    for (int idx = tid; idx < GP * D; idx += NT) {
         const int h = idx / D, d = idx % D;
         float x = 0.f;
         if (h < G) x = Elem<QT>::to_f32(p.q[b * p.q_bstride + (kvh * G + h) * p.q_hstride + d]);
         smem[idx] = x;
     }
     if (owner) {
-        for (int d = tid; d < D; d += 256) {
+        for (int d = tid; d < D; d += NT) {
             const int64_t o = (static_cast<int64_t>(b) * p.Hkv + kvh) * D + d;
             kn_s[d] = bf16_bits_to_f32(p.k_new[o]);
             vn_s[d] = bf16_bits_to_f32(p.v_new[o]);
@@ -193,7 +219,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     if (p.fused) {
         // Per-head RMSNorm with (1 + w), bf16 result (full_attention_4b.hip:5142-5191).
         const int rows = G + (owner ? 1 : 0);
-        for (int r = wave; r < rows; r += 4) {
+        for (int r = wave; r < rows; r += NW) {
             float* row = r < G ? &smem[r * D] : kn_s;
             const uint16_t* w = r < G ? p.q_norm_w : p.k_norm_w;
             float ss = 0.f;
@@ -209,7 +235,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
         if (hr > 0) {
             const uint16_t* ct = p.cos_t + static_cast<int64_t>(pos) * hr;
             const uint16_t* st = p.sin_t + static_cast<int64_t>(pos) * hr;
-            for (int idx = tid; idx < rows * hr; idx += 256) {
+            for (int idx = tid; idx < rows * hr; idx += NT) {
                 const int r = idx / hr, i = idx % hr;
                 float* row = r < G ? &smem[r * D] : kn_s;
                 const float c = bf16_bits_to_f32(ct[i]), s = bf16_bits_to_f32(st[i]);
@@ -225,7 +251,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
             if constexpr (!FP8) {
                 uint16_t* kc = reinterpret_cast<uint16_t*>(p.kv.k) + off;
                 uint16_t* vc = reinterpret_cast<uint16_t*>(p.kv.v) + off;
-                for (int d = tid; d < D; d += 256) {
+                for (int d = tid; d < D; d += NT) {
                     kc[d] = static_cast<uint16_t>(f32_to_bf16_bits(kn_s[d]));
                     vc[d] = static_cast<uint16_t>(f32_to_bf16_bits(vn_s[d]));
                 }
@@ -274,6 +300,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     __syncthreads();  // smem is reused by the merge below
 
     // ---------------------------------------------------------------- main loop
+    SSA_DSTAMP(1);
     float m[4], lsum[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) { m[i] = -1e30f; lsum[i] = 0.f; }
@@ -407,15 +434,31 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
 
     // Software pipeline: the next block's loads are in flight while the
     // current block is computed (two register sets, unrolled by two).
+    // Blocks are claimed from an LDS counter (wave w starts with block w), so
+    // a wave whose loads are served more slowly simply takes fewer blocks and
+    // the waves of the workgroup finish together.
+    auto take = [&]() {
+        int v = 0;
+        if (lane == 0) v = atomicAdd(&next_blk, 1);
+        return __builtin_amdgcn_readfirstlane(v);
+    };
     {
         Blk A, Bn;
-        if (wave < nblk) fetch(wave, A);
-        for (int blk = wave; blk < nblk; blk += 8) {
-            if (blk + 4 < nblk) fetch(blk + 4, Bn);
-            process_blk(blk, A);
-            if (blk + 4 >= nblk) break;
-            if (blk + 8 < nblk) fetch(blk + 8, A);
-            process_blk(blk + 4, Bn);
+        int c0 = wave, c1 = nblk;
+        if (c0 < nblk) {
+            fetch(c0, A);
+            c1 = take();
+            if (c1 < nblk) fetch(c1, Bn);
+        }
+        while (c0 < nblk) {
+            process_blk(c0, A);
+            if (c1 >= nblk) break;
+            c0 = take();
+            if (c0 < nblk) fetch(c0, A);
+            process_blk(c1, Bn);
+            if (c0 >= nblk) break;
+            c1 = take();
+            if (c1 < nblk) fetch(c1, Bn);
         }
     }
     // The new token (fused owner split): one more block of one token, read
@@ -438,6 +481,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     }
 
     // ---------------------------------------------------------------- merge
+    SSA_DSTAMP(2);
     float ltot[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
@@ -462,7 +506,9 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     float fw[GP];
 #pragma unroll
     for (int h = 0; h < GP; ++h) {
-        float M = fmaxf(fmaxf(ml_s[0][h][0], ml_s[1][h][0]), fmaxf(ml_s[2][h][0], ml_s[3][h][0]));
+        float M = ml_s[0][h][0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
         fw[h] = exp2f(ml_s[wave][h][0] - M);
     }
 #pragma unroll
@@ -470,28 +516,25 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
 
-    // Two LDS rounds: waves 2,3 -> 0,1, then wave 1 -> 0.
-    if (wave >= 2 && lane < LPT) {
+    // LDS tree: waves [half, 2 half) add into waves [0, half), until wave 0
+    // holds the workgroup's sum.
 #pragma unroll
-        for (int h = 0; h < GP; ++h)
+    for (int half = NW / 2; half >= 1; half /= 2) {
+        if (wave >= half && wave < 2 * half && lane < LPT) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) smem[((wave - 2) * GP + h) * D + vd + e] = acc[h][e];
+            for (int h = 0; h < GP; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) smem[((wave - half) * GP + h) * D + vd + e] = acc[h][e];
+        }
+        __syncthreads();
+        if (wave < half && lane < LPT) {
+#pragma unroll
+            for (int h = 0; h < GP; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] += smem[(wave * GP + h) * D + vd + e];
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (wave < 2 && lane < LPT) {
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] += smem[(wave * GP + h) * D + vd + e];
-    }
-    __syncthreads();
-    if (wave == 1 && lane < LPT) {
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) smem[h * D + vd + e] = acc[h][e];
-    }
-    __syncthreads();
     if (wave == 0) {
         if (lane < LPT) {
 #pragma unroll
@@ -499,7 +542,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
                 if (h < G) {
                     float o[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] = acc[h][e] + smem[h * D + vd + e];
+                    for (int e = 0; e < 8; ++e) o[e] = acc[h][e];
                     const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
                     float* dst = p.part_o + row * D + vd;
 #pragma unroll
@@ -511,10 +554,10 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
             const int h = lane;
             float M = -1e30f;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) M = fmaxf(M, ml_s[w][h][0]);
+            for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
             float L = 0.f;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) L += exp2f(ml_s[w][h][0] - M) * ml_s[w][h][1];
+            for (int w = 0; w < NW; ++w) L += exp2f(ml_s[w][h][0] - M) * ml_s[w][h][1];
             const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
             store_agent(&p.part_ml[2 * row], M);
             store_agent(&p.part_ml[2 * row + 1], L);
@@ -522,6 +565,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
     }
 
     // ---------------------------------------------------------------- split merge
+    SSA_DSTAMP(3);
     // The last split of (b, kv head) to arrive merges all of them (log-sum-exp)
     // and applies the gate.  The partials are written and read with device-
     // coherent (sc1) accesses, and the writer waits for its stores to complete
@@ -536,8 +580,9 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
         last_s = prev == static_cast<unsigned>(ns - 1);
     }
     __syncthreads();
+    SSA_DSTAMP(4);
     if (!last_s) return;
-    for (int hh = wave; hh < G; hh += 4) {
+    for (int hh = wave; hh < G; hh += NW) {
         const int h = kvh * G + hh;
         const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + h) * p.nsplit;
         // One online pass over the splits, MCH at a time with all their loads
@@ -587,6 +632,7 @@ __global__ __launch_bounds__(256, GP <= 8 ? 2 : 1) void decode_split_kernel(Deco
             store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + d, r);
         }
     }
+    SSA_DSTAMP(5);
     if (tid == 0) p.arrivals[b * p.Hkv + kvh] = 0u;  // every split has arrived: ready for the next call
 }
 
@@ -606,8 +652,9 @@ static int env_int(const char* name, int dflt) {
 
 // Chunk of tokens per workgroup: enough workgroups to fill 256 CUs a few
 // times over, but chunks of at least 64 tokens (4 waves x 16).
-static SplitPlan plan_splits(int B, int Hkv, int max_len) {
-    const int target = env_int("SUPERSONIC_DECODE_TARGET_WGS", 512);
+static SplitPlan plan_splits(int B, int Hkv, int max_len, int waves) {
+    // 2048 resident waves: one 8-wave or two 4-wave workgroups per CU
+    const int target = env_int("SUPERSONIC_DECODE_TARGET_WGS", 2048 / waves);
     const int min_chunk = env_int("SUPERSONIC_DECODE_MIN_CHUNK", 128);
     const int pairs = B * Hkv;
     int want = (target + pairs - 1) / pairs;
@@ -641,9 +688,9 @@ static size_t workspace_bytes_for(int B, int Hq, int D, int nsplit) {
 template <typename QT, bool FP8, int D>
 static hipError_t launch_split(dim3 grid, hipStream_t st, int GP, const DecodeParams& p) {
     switch (GP) {
-    case 4: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 4>), grid, dim3(256), 0, st, p); break;
-    case 8: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 8>), grid, dim3(256), 0, st, p); break;
-    default: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 16>), grid, dim3(256), 0, st, p); break;
+    case 4: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 4>), grid, dim3(64 * decode_waves(4)), 0, st, p); break;
+    case 8: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 8>), grid, dim3(64 * decode_waves(8)), 0, st, p); break;
+    default: hipLaunchKernelGGL((decode_split_kernel<QT, FP8, D, 16>), grid, dim3(64 * decode_waves(16)), 0, st, p); break;
     }
     return hipGetLastError();
 }
@@ -684,7 +731,7 @@ static int run_decode(DecodeRequest& r) {
     if (r.B <= 0) return 0;
     if (static_cast<int64_t>(r.B) * r.Hkv > kMaxArrivals) return SUPERSONIC_ERR_RANGE;
     if (r.max_len <= 0) r.max_len = 1;
-    const SplitPlan sp = plan_splits(r.B, r.Hkv, r.max_len);
+    const SplitPlan sp = plan_splits(r.B, r.Hkv, r.max_len, decode_waves(GP));
     const size_t need = workspace_bytes_for(r.B, r.Hq, r.D, sp.nsplit);
     void* ws = r.workspace;
     if (ws) {
@@ -799,6 +846,12 @@ static int decode_flat_common(int dtype, size_t device, size_t B, size_t Hq, siz
 
 using namespace ssa;
 
+#ifdef SSA_TRACE
+extern "C" int ssa_decode_trace_dump(void* dst) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(ssa::g_decode_trace), sizeof(ssa::g_decode_trace)) == hipSuccess ? 0 : 1;
+}
+#endif
+
 extern "C" int supersonic_qwen35_hip_full_attention_decode_flat(
     int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
     size_t kv_len, size_t head_dim, size_t num_kv_groups, float scale,
@@ -819,8 +872,10 @@ extern "C" int supersonic_qwen35_hip_full_attention_decode_flat_strided(
 extern "C" size_t supersonic_attn_gfx950_decode_workspace_size(
     size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len) {
     if (kv_heads == 0) return 0;
+    const size_t G = q_heads / kv_heads;
+    const int GP = G <= 4 ? 4 : (G <= 8 ? 8 : 16);
     const SplitPlan sp = plan_splits(static_cast<int>(batch), static_cast<int>(kv_heads),
-                                     max_kv_len ? static_cast<int>(max_kv_len) : 1);
+                                     max_kv_len ? static_cast<int>(max_kv_len) : 1, decode_waves(GP));
     return workspace_bytes_for(static_cast<int>(batch), static_cast<int>(q_heads), static_cast<int>(head_dim),
                                sp.nsplit);
 }
