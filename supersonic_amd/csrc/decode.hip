@@ -202,75 +202,102 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
 
     // ---------------------------------------------------------------- prologue
     if (tid == 0) next_blk = NW;  // blocks 0 .. NW-1 are the waves' first
-    for (int idx = tid; idx < GP * D; idx += NT) {
-        const int h = idx / D, d = idx % D;
-        float x = 0.f;
-        if (h < G) x = Elem<QT>::to_f32(p.q[b * p.q_bstride + (kvh * G + h) * p.q_hstride + d]);
-        smem[idx] = x;
-    }
-    if (owner) {
-        for (int d = tid; d < D; d += NT) {
-            const int64_t o = (static_cast<int64_t>(b) * p.Hkv + kvh) * D + d;
-            kn_s[d] = bf16_bits_to_f32(p.k_new[o]);
-            vn_s[d] = bf16_bits_to_f32(p.v_new[o]);
-        }
-    }
-    __syncthreads();
-    if (p.fused) {
-        // Per-head RMSNorm with (1 + w), bf16 result (full_attention_4b.hip:5142-5191).
+    // One wave per row: rows 0 .. G-1 are the q heads, row G (owner split of
+    // the fused step) is the new k (with v alongside).  Lane l holds dims
+    // l + 64 k.  All global loads of a row go out before any arithmetic, so the
+    // prologue costs one memory round trip.
+    {
+        constexpr int EPL = D / 64;
+        const int hr = p.fused ? p.half_rot : 0;
         const int rows = G + (owner ? 1 : 0);
         for (int r = wave; r < rows; r += NW) {
-            float* row = r < G ? &smem[r * D] : kn_s;
-            const uint16_t* w = r < G ? p.q_norm_w : p.k_norm_w;
-            float ss = 0.f;
-            for (int d = lane; d < D; d += 64) ss += row[d] * row[d];
-            ss = wave_sum(ss);
-            const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
-            for (int d = lane; d < D; d += 64)
-                row[d] = bf16_round(row[d] * inv * (bf16_bits_to_f32(w[d]) + 1.0f));
-        }
-        __syncthreads();
-        // Rotate-half partial RoPE at the new token's position (:5193-5224).
-        const int hr = p.half_rot;
-        if (hr > 0) {
-            const uint16_t* ct = p.cos_t + static_cast<int64_t>(pos) * hr;
-            const uint16_t* st = p.sin_t + static_cast<int64_t>(pos) * hr;
-            for (int idx = tid; idx < rows * hr; idx += NT) {
-                const int r = idx / hr, i = idx % hr;
-                float* row = r < G ? &smem[r * D] : kn_s;
-                const float c = bf16_bits_to_f32(ct[i]), s = bf16_bits_to_f32(st[i]);
-                const float x0 = row[i], x1 = row[i + hr];
-                row[i] = bf16_round(x0 * c - x1 * s);
-                row[i + hr] = bf16_round(x0 * s + x1 * c);
+            const bool is_k = r == G;
+            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                const int d = lane + 64 * k;
+                if (!is_k) {
+                    x[k] = Elem<QT>::to_f32(p.q[b * p.q_bstride + (kvh * G + r) * p.q_hstride + d]);
+                } else {
+                    const int64_t o = (static_cast<int64_t>(b) * p.Hkv + kvh) * D + d;
+                    x[k] = bf16_bits_to_f32(p.k_new[o]);
+                    vx[k] = bf16_bits_to_f32(p.v_new[o]);
+                }
+                if (p.fused) w[k] = bf16_bits_to_f32((is_k ? p.k_norm_w : p.q_norm_w)[d]);
+                cs[k] = sn[k] = 0.f;
+                if (d < 2 * hr) {
+                    const int64_t ti = static_cast<int64_t>(pos) * hr + (d < hr ? d : d - hr);
+                    cs[k] = bf16_bits_to_f32(p.cos_t[ti]);
+                    sn[k] = bf16_bits_to_f32(p.sin_t[ti]);
+                }
+            }
+            float* row = is_k ? kn_s : &smem[r * D];
+            if (p.fused) {
+                // Per-head RMSNorm with (1 + w), bf16 result (full_attention_4b.hip:5142-5191).
+                float ss = 0.f;
+#pragma unroll
+                for (int k = 0; k < EPL; ++k) ss += x[k] * x[k];
+                ss = wave_sum(ss);
+                const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
+#pragma unroll
+                for (int k = 0; k < EPL; ++k) x[k] = bf16_round(x[k] * inv * (w[k] + 1.0f));
+                // Rotate-half partial RoPE at the new token's position (:5193-5224);
+                // the partner of dim d < 2 hr is d +- hr, read from the row in LDS.
+                if (hr > 0) {
+#pragma unroll
+                    for (int k = 0; k < EPL; ++k) row[lane + 64 * k] = x[k];
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                    for (int k = 0; k < EPL; ++k) {
+                        const int d = lane + 64 * k;
+                        if (d < 2 * hr) {
+                            const float other = row[d < hr ? d + hr : d - hr];
+                            x[k] = d < hr ? bf16_round(x[k] * cs[k] - other * sn[k])
+                                          : bf16_round(other * sn[k] + x[k] * cs[k]);
+                        }
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                row[lane + 64 * k] = x[k];
+                if (is_k) vn_s[lane + 64 * k] = vx[k];
             }
         }
-        __syncthreads();
+        // heads G .. GP-1 are zero rows of the padded MFMA operand
+        for (int idx = G * D + tid; idx < GP * D; idx += NT) smem[idx] = 0.f;
+    }
+    __syncthreads();
+    if (p.fused && owner) {
         // KV append at slot pos (:5226-5296); FP8 uses the absmax scale and OCP e4m3.
-        if (owner) {
-            const int64_t off = p.kv.row(b, kvh, pos, D);
-            if constexpr (!FP8) {
-                uint16_t* kc = reinterpret_cast<uint16_t*>(p.kv.k) + off;
-                uint16_t* vc = reinterpret_cast<uint16_t*>(p.kv.v) + off;
-                for (int d = tid; d < D; d += NT) {
-                    kc[d] = static_cast<uint16_t>(f32_to_bf16_bits(kn_s[d]));
-                    vc[d] = static_cast<uint16_t>(f32_to_bf16_bits(vn_s[d]));
+        const int64_t off = p.kv.row(b, kvh, pos, D);
+        if constexpr (!FP8) {
+            uint16_t* kc = reinterpret_cast<uint16_t*>(p.kv.k) + off;
+            uint16_t* vc = reinterpret_cast<uint16_t*>(p.kv.v) + off;
+            for (int d = tid; d < D; d += NT) {
+                kc[d] = static_cast<uint16_t>(f32_to_bf16_bits(kn_s[d]));
+                vc[d] = static_cast<uint16_t>(f32_to_bf16_bits(vn_s[d]));
+            }
+        } else {
+            if (wave < 2) {
+                const float* src = wave == 0 ? kn_s : vn_s;
+                uint8_t* dst = (wave == 0 ? p.kv.k : p.kv.v) + off;
+                float am = 0.f;
+                for (int d = lane; d < D; d += 64) am = fmaxf(am, fabsf(src[d]));
+                am = wave_max(am);
+                const float sc = fmaxf(am / 448.0f, 1e-12f);
+                const float inv = 1.0f / sc;
+                for (int d = lane * 4; d < D; d += 256) {
+                    const uint32_t c4 = f32x4_to_fp8x4(src[d] * inv, src[d + 1] * inv,
+                                                       src[d + 2] * inv, src[d + 3] * inv);
+                    *reinterpret_cast<uint32_t*>(dst + d) = c4;
                 }
-            } else {
-                if (wave < 2) {
-                    const float* src = wave == 0 ? kn_s : vn_s;
-                    uint8_t* dst = (wave == 0 ? p.kv.k : p.kv.v) + off;
-                    float am = 0.f;
-                    for (int d = lane; d < D; d += 64) am = fmaxf(am, fabsf(src[d]));
-                    am = wave_max(am);
-                    const float sc = fmaxf(am / 448.0f, 1e-12f);
-                    const float inv = 1.0f / sc;
-                    for (int d = lane * 4; d < D; d += 256) {
-                        const uint32_t c4 = f32x4_to_fp8x4(src[d] * inv, src[d + 1] * inv,
-                                                           src[d + 2] * inv, src[d + 3] * inv);
-                        *reinterpret_cast<uint32_t*>(dst + d) = c4;
-                    }
-                    if (lane == 0) (wave == 0 ? p.kv.ks : p.kv.vs)[p.kv.srow(b, kvh, pos)] = sc;
-                }
+                if (lane == 0) (wave == 0 ? p.kv.ks : p.kv.vs)[p.kv.srow(b, kvh, pos)] = sc;
             }
         }
     }
