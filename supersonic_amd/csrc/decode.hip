@@ -174,7 +174,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
 
     constexpr int NW = decode_waves(GP);
     constexpr int NT = 64 * NW;
-    __shared__ float smem[(NW / 2 > 2 ? NW / 2 : 2) * GP * D];  // q staging, then the wave merge
+    __shared__ float smem[NW * GP * D];        // q staging, then the wave merge
     __shared__ float p_s[NW][16][GP];          // per-wave probabilities
     __shared__ float kn_s[D], vn_s[D];         // the new token (fused owner split)
     __shared__ float ml_s[NW][GP][2];
@@ -543,40 +543,24 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
 
-    // LDS tree: waves [half, 2 half) add into waves [0, half), until wave 0
-    // holds the workgroup's sum.
+    // One LDS round: every wave parks its scaled sums in its own slot, then
+    // the whole workgroup adds the NW slots and writes the split's partials.
+    if (lane < LPT) {
 #pragma unroll
-    for (int half = NW / 2; half >= 1; half /= 2) {
-        if (wave >= half && wave < 2 * half && lane < LPT) {
+        for (int h = 0; h < GP; ++h)
 #pragma unroll
-            for (int h = 0; h < GP; ++h)
+            for (int e = 0; e < 8; ++e) smem[(wave * GP + h) * D + vd + e] = acc[h][e];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * D; idx += NT) {
+        const int h = idx / D, d = idx % D;
+        float o = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) smem[((wave - half) * GP + h) * D + vd + e] = acc[h][e];
-        }
-        __syncthreads();
-        if (wave < half && lane < LPT) {
-#pragma unroll
-            for (int h = 0; h < GP; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] += smem[(wave * GP + h) * D + vd + e];
-        }
-        __syncthreads();
+        for (int w = 0; w < NW; ++w) o += smem[(w * GP + h) * D + d];
+        const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
+        store_agent(p.part_o + row * D + d, o);
     }
     if (wave == 0) {
-        if (lane < LPT) {
-#pragma unroll
-            for (int h = 0; h < GP; ++h) {
-                if (h < G) {
-                    float o[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] = acc[h][e];
-                    const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
-                    float* dst = p.part_o + row * D + vd;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) store_agent(dst + e, o[e]);
-                }
-            }
-        }
         if (lane < G) {
             const int h = lane;
             float M = -1e30f;
