@@ -29,6 +29,19 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_JSON = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the workload's dominant kernel, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (calibrated against a
+    plain copy; profiles/traffic_pmc_decode_prefill.md holds the commands), or
+    None when no measurement is on file."""
+    try:
+        with open(TRAFFIC_JSON) as f:
+            return json.load(f).get(workload, {}).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
 MALL_BYTES = 256 << 20
 
 
@@ -188,10 +201,11 @@ class Workloads:
                            head_dim=D, rotary_dim=rot, max_kv_len=max(lens) + 1, workspace=args["ws"])
         return step, n_copies
 
-    def decode_result(self, name, B, lens, Hq, Hkv, D, rot, fp8=False, paged_ps=None, cap=None):
+    def decode_result(self, name, B, lens, Hq, Hkv, D, rot, fp8=False, paged_ps=None, cap=None, traffic_key=None):
         step, n = self.make_decode(B, lens, Hq, Hkv, D, rot, fp8=fp8, paged_ps=paged_ps, cap=cap)
         step_ms, kern_ms, _ = self.timed(step, n)
         kv_bytes, bytes_step = self.decode_bytes(lens, Hq, Hkv, D, 1 if fp8 else 2, 4 if fp8 else 0)
+        traffic = measured_traffic(traffic_key) if traffic_key else None
         # dominant kernel's algorithmic bytes: K+V (+scales) and q
         kern_bytes = kv_bytes + B * Hq * D * 2
         ach = kern_bytes / (kern_ms * 1e-3) / 1e9
@@ -200,13 +214,13 @@ class Workloads:
             "workload": name, "gbs": bytes_step / (step_ms * 1e-3) / 1e9, "ms_per_step": step_ms,
             "bytes": bytes_step, "kernel_ms": kern_ms, "cache_copies": n,
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                          "kernel": "decode_split_kernel", "bytes_per_launch": kern_bytes},
         }
 
     # ------------------------------------------------------------ workloads
     def decode8(self):
-        return self.decode_result("config 2, B=8, L=32768", 8, [32768] * 8, 16, 4, 256, 64)
+        return self.decode_result("config 2, B=8, L=32768", 8, [32768] * 8, 16, 4, 256, 64, traffic_key="decode8")
 
     def decode1(self):
         r = self.decode_result("config 2, B=1, L=32768", 1, [32768], 16, 4, 256, 64)
@@ -263,8 +277,8 @@ class Workloads:
                 "tflops_step": fl / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms, "kernel_ms": kern_ms,
                 "flops": fl,
                 "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                             "kernel": "prefill_kernel"}}
+                             "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+                             "traffic": measured_traffic("prefill"), "kernel": "prefill_kernel"}}
 
     def mixed(self):
         """Config 5: one 8192-token prefill chunk + 32 decode sequences, 16/2 heads,
