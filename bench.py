@@ -14,7 +14,7 @@ larger than the 256 MB last-level cache, so every step streams HBM.
 ``roofline`` is for the dominant kernel (``decode_split_kernel``), timed live
 with HIP events recorded on its launch stream around each launch.
 ``cpu_baseline`` is the repo's torch fp32 oracle timed on this host for the
-same workload.  ``extra`` holds the other BASELINE configs (decode B=1,
+same workload.  ``extra`` holds the other BASELINE configs (config 1 decode, config 2 B=1,
 causal prefill at 4096 tokens, FP8-KV ragged decode, mixed paged batch).
 """
 from __future__ import annotations
@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
-    ap.add_argument("--only", default="", help="run one workload: decode8|decode1|prefill|fp8|mixed|copy")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|copy")
     return ap.parse_args()
 
 
@@ -104,7 +104,7 @@ def main():
     if not args.skip_cpu:
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
-        out["extra"] = {k: getattr(W, k)() for k in ("decode1", "prefill", "fp8", "mixed")}
+        out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "fp8", "mixed")}
     print(json.dumps(out))
 
 
@@ -221,6 +221,12 @@ class Workloads:
     # ------------------------------------------------------------ workloads
     def decode8(self):
         return self.decode_result("config 2, B=8, L=32768", 8, [32768] * 8, 16, 4, 256, 64, traffic_key="decode8")
+
+    def decode_cfg1(self):
+        """Config 1: Qwen3.5-0.8B-like decode, B=1, 8/2 heads, 2048 cached tokens."""
+        r = self.decode_result("config 1, B=1, Hq 8, Hkv 2, L=2048", 1, [2048], 8, 2, 256, 64)
+        r["gbs"] = round(r["gbs"], 2)
+        return r
 
     def decode1(self):
         r = self.decode_result("config 2, B=1, L=32768", 1, [32768], 16, 4, 256, 64)
