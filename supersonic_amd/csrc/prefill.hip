@@ -209,7 +209,21 @@ __device__ unsigned long long g_prefill_trace[16 * 2 * 64 * 6];
             __builtin_amdgcn_sched_barrier(0);                                                             \
         }                                                                                                  \
     } while (0)
+// Workgroup timeline: s_memrealtime at entry (slot 0), after the query
+// prologue (1), after the key loop (2) and at exit (3), plus the hardware id.
+__device__ unsigned long long g_prefill_wg[4096 * 6];
+#define SSA_WG_STAMP(slot)                                                                          \
+    do {                                                                                            \
+        if (tid == 0 && blockIdx.x < 4096) {                                                        \
+            g_prefill_wg[blockIdx.x * 6 + (slot)] = __builtin_amdgcn_s_memrealtime();               \
+            if ((slot) == 0) g_prefill_wg[blockIdx.x * 6 + 4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)); \
+            if ((slot) == 0) g_prefill_wg[blockIdx.x * 6 + 5] = ntiles;                            \
+        }                                                                                           \
+    } while (0)
 #else
+#define SSA_WG_STAMP(slot) \
+    do {                   \
+    } while (0)
 #define SSA_STAMP(slot) \
     do {                \
     } while (0)
@@ -302,6 +316,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                                                      16, (i & 1) ? vt_lane1 : vt_lane0, 8 * i * vt_rowb, 0, 0);
         }
     };
+    SSA_WG_STAMP(0);
     if (wave >= kPrefillWaves) {
         // Copy waves: tile it goes to stage (it + 1) & 1; the next tile is
         // issued once everyone has passed the barrier of tile it (its stage's
@@ -326,48 +341,86 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         for (int s = 0; s < KS; ++s)
             qb[s] = to_op<op_t>(row_ok ? ld16(qrow + 32 * s + 8 * g4) : u32x4_v{0u, 0u, 0u, 0u});
     } else {
-        // Stage this wave's 16 query rows in LDS (stage 0), RMSNorm with
-        // (1 + w) and rotate-half RoPE at position off + row, bf16 after each
-        // step (prefill_engine.rs:2025-2096), then read the operand back.
+        // This wave's 16 query rows: RMSNorm with (1 + w) and rotate-half RoPE
+        // at position off + row, bf16 after each step (prefill_engine.rs:2025-2096),
+        // (lane c of a row holds dims 8c .. 8c+7); every global load is issued
+        // before any arithmetic.  The rows are staged in LDS (stage 0), where
+        // the RoPE partner dims are read back and the operand is read
+        // transposed.
         uint16_t* qs = reinterpret_cast<uint16_t*>(lds) + wave * 16 * D;
         constexpr int LPR = D / 8;              // lanes per row, 16 B each
         constexpr int RPI = 64 / LPR;           // rows per instruction
-        for (int r0 = 0; r0 < 16; r0 += RPI) {
-            const int r = r0 + lane / LPR, c = lane % LPR;
-            const int row = row_w0 + r;
-            u32x4_v w = {0u, 0u, 0u, 0u};
-            if (row < S) w = ld16(p.q + h * p.q_hs + static_cast<int64_t>(row) * p.q_rs + 8 * c);
+        constexpr int NIN = 16 / RPI;           // instructions per wave
+        const int c = lane % LPR, rr = lane / LPR;
+        const int hr = p.half_rot;              // a multiple of 16 (checked on the host)
+        const bool rot = 8 * c < 2 * hr;
+        const u32x4_v wtw = ld16(p.q_norm_w + 8 * c);
+        u32x4_v qw[NIN], cw[NIN], sw[NIN];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) {
+            const int row = row_w0 + k * RPI + rr;
+            qw[k] = cw[k] = sw[k] = u32x4_v{0u, 0u, 0u, 0u};
+            if (row < S) {
+                qw[k] = ld16(p.q + h * p.q_hs + static_cast<int64_t>(row) * p.q_rs + 8 * c);
+                if (rot) {
+                    const int64_t ti = static_cast<int64_t>(off + row) * hr + (8 * c < hr ? 8 * c : 8 * c - hr);
+                    cw[k] = ld16(p.cos_t + ti);
+                    sw[k] = ld16(p.sin_t + ti);
+                }
+            }
+        }
+        float wt[8];
+        unpack8<bf16_t>(wtw, wt);
+        // RMSNorm: the row's sum of squares over its LPR lanes on the VALU
+        // (DPP within 16 lanes, a permlane swap across 16), no LDS traffic.
+        u32x4_v nq[NIN];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) {
             float x[8];
-            unpack8<bf16_t>(w, x);
+            unpack8<bf16_t>(qw[k], x);
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+            if constexpr (LPR >= 16) {
+                ss = row16_sum(ss);
+                if constexpr (LPR == 32) ss = xor16_sum(ss);
+            } else {
 #pragma unroll
-            for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
+                for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
+            }
             const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
-            float wt[8];
-            unpack8<bf16_t>(ld16(p.q_norm_w + 8 * c), wt);
-            u32x4_v o;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                o[j] = pk2<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
-            st16(qs + r * D + 8 * c, o);
+                nq[k][j] = pk2<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
+            st16(qs + (k * RPI + rr) * D + 8 * c, nq[k]);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int hr = p.half_rot;
-        for (int idx = lane; idx < 16 * hr; idx += 64) {
-            const int r = idx / hr, i = idx % hr;
-            const int row = row_w0 + r;
-            if (row < S) {
-                const int pos = off + row;
-                const float c = bf16_bits_to_f32(p.cos_t[static_cast<int64_t>(pos) * hr + i]);
-                const float sn = bf16_bits_to_f32(p.sin_t[static_cast<int64_t>(pos) * hr + i]);
-                const float x0 = bf16_bits_to_f32(qs[r * D + i]);
-                const float x1 = bf16_bits_to_f32(qs[r * D + i + hr]);
-                qs[r * D + i] = static_cast<uint16_t>(f32_to_bf16_bits(x0 * c - x1 * sn));
-                qs[r * D + i + hr] = static_cast<uint16_t>(f32_to_bf16_bits(x0 * sn + x1 * c));
+        if (hr > 0) {
+            // RoPE: the rotating lanes read their partner's 8 normed dims back
+            // (all reads are issued before any write; LDS is in order per wave).
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int pc = 8 * c < hr ? 8 * c + hr : 8 * c - hr;
+            u32x4_v yq[NIN];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k)
+                yq[k] = rot ? ld16(qs + (k * RPI + rr) * D + pc) : u32x4_v{0u, 0u, 0u, 0u};
+            if (rot) {
+#pragma unroll
+                for (int k = 0; k < NIN; ++k) {
+                    float x[8], y[8], cs[8], sn[8];
+                    unpack8<bf16_t>(nq[k], x);
+                    unpack8<bf16_t>(yq[k], y);
+                    unpack8<bf16_t>(cw[k], cs);
+                    unpack8<bf16_t>(sw[k], sn);
+                    const float sg = 8 * c < hr ? -1.0f : 1.0f;
+                    u32x4_v o;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        o[j] = pk2<bf16_t>(x[2 * j] * cs[2 * j] + sg * y[2 * j] * sn[2 * j],
+                                           x[2 * j + 1] * cs[2 * j + 1] + sg * y[2 * j + 1] * sn[2 * j + 1]);
+                    st16(qs + (k * RPI + rr) * D + 8 * c, o);
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -397,6 +450,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const int vrd0 = T::KBYTES + 16 * (8 * (lane & 15) + (g4 ^ vx));
     const int vrd1 = T::KBYTES + 16 * (8 * (lane & 15) + ((4 + g4) ^ vx));
 
+    SSA_WG_STAMP(1);
     for (int it = 0; it < ntiles; ++it) {
         const int k0 = it * 64;
         const int st = (it + 1) & 1;
@@ -507,6 +561,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         SSA_STAMP(4);
     }
 
+    SSA_WG_STAMP(2);
     // ------------------------------------------------ epilogue
     // O^T C layout: lane holds row myrow, dims 16 d + 4 g4 + i.
     const float l_tot = lacc[0];
@@ -523,10 +578,15 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         // bf16(attn) * sigmoid(gate), bf16 out [S, Hq*D] (prefill_engine.rs:2263-2308).
         uint16_t* orow = p.out_bf16 + static_cast<int64_t>(myrow) * p.Hq * D + h * D;
         const uint16_t* grow = p.gate + h * p.q_hs + static_cast<int64_t>(myrow) * p.q_rs;
+        // all gate loads first (the output stores could alias them as far as
+        // the compiler knows, which would serialise one load per store)
+        u32x2_v gwa[DBK];
+#pragma unroll
+        for (int d = 0; d < DBK; ++d) gwa[d] = *reinterpret_cast<const u32x2_v*>(grow + 16 * d + 4 * g4);
 #pragma unroll
         for (int d = 0; d < DBK; ++d) {
             const int dd = 16 * d + 4 * g4;
-            const u32x2_v gw = *reinterpret_cast<const u32x2_v*>(grow + dd);
+            const u32x2_v gw = gwa[d];
             const float gv[4] = {bf16_bits_to_f32(gw[0] & 0xFFFFu), bf16_bits_to_f32(gw[0] >> 16),
                                  bf16_bits_to_f32(gw[1] & 0xFFFFu), bf16_bits_to_f32(gw[1] >> 16)};
             float r[4];
@@ -541,6 +601,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
             *reinterpret_cast<u32x2_v*>(orow + dd) = o;
         }
     }
+    SSA_WG_STAMP(3);
 #endif
 }
 
@@ -814,6 +875,9 @@ static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t 
 using namespace ssa;
 
 #ifdef SSA_TRACE
+extern "C" int ssa_prefill_wg_dump(void* dst) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(ssa::g_prefill_wg), sizeof(ssa::g_prefill_wg)) == hipSuccess ? 0 : 1;
+}
 extern "C" int ssa_prefill_trace_dump(void* dst) {
     return hipMemcpyFromSymbol(dst, HIP_SYMBOL(ssa::g_prefill_trace), sizeof(ssa::g_prefill_trace)) == hipSuccess ? 0 : 1;
 }
