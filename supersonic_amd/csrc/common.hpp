@@ -26,12 +26,10 @@ typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-// Round-to-nearest-even f32 -> bf16 bits (finite inputs; NaN kept quiet).
+// Round-to-nearest-even f32 -> bf16 bits with the hardware converter
+// (v_cvt_pk_bf16_f32; a NaN stays a quiet NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu)) return (u >> 16) | 0x40u;
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
 __device__ __forceinline__ float bf16_round(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
 

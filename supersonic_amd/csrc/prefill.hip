@@ -210,14 +210,15 @@ __device__ unsigned long long g_prefill_trace[16 * 2 * 64 * 6];
         }                                                                                                  \
     } while (0)
 // Workgroup timeline: s_memrealtime at entry (slot 0), after the query
-// prologue (1), after the key loop (2) and at exit (3), plus the hardware id.
-__device__ unsigned long long g_prefill_wg[4096 * 6];
+// prologue (1), after the key loop (2) and at exit (3), the hardware id (4),
+// the tile count (5), after the query norm (6) and after the query RoPE (7).
+__device__ unsigned long long g_prefill_wg[4096 * 8];
 #define SSA_WG_STAMP(slot)                                                                          \
     do {                                                                                            \
         if (tid == 0 && blockIdx.x < 4096) {                                                        \
-            g_prefill_wg[blockIdx.x * 6 + (slot)] = __builtin_amdgcn_s_memrealtime();               \
-            if ((slot) == 0) g_prefill_wg[blockIdx.x * 6 + 4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)); \
-            if ((slot) == 0) g_prefill_wg[blockIdx.x * 6 + 5] = ntiles;                            \
+            g_prefill_wg[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memrealtime();               \
+            if ((slot) == 0) g_prefill_wg[blockIdx.x * 8 + 4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)); \
+            if ((slot) == 0) g_prefill_wg[blockIdx.x * 8 + 5] = ntiles;                            \
         }                                                                                           \
     } while (0)
 #else
@@ -391,9 +392,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
             const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                nq[k][j] = pk2<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
+                nq[k][j] = cvt_pk<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
             st16(qs + (k * RPI + rr) * D + 8 * c, nq[k]);
         }
+        SSA_WG_STAMP(6);
         if (hr > 0) {
             // RoPE: the rotating lanes read their partner's 8 normed dims back
             // (all reads are issued before any write; LDS is in order per wave).
@@ -417,12 +419,13 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                     u32x4_v o;
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        o[j] = pk2<bf16_t>(x[2 * j] * cs[2 * j] + sg * y[2 * j] * sn[2 * j],
+                        o[j] = cvt_pk<bf16_t>(x[2 * j] * cs[2 * j] + sg * y[2 * j] * sn[2 * j],
                                            x[2 * j + 1] * cs[2 * j + 1] + sg * y[2 * j + 1] * sn[2 * j + 1]);
                     st16(qs + (k * RPI + rr) * D + 8 * c, o);
                 }
             }
         }
+        SSA_WG_STAMP(7);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
