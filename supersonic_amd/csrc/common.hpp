@@ -179,6 +179,9 @@ constexpr int kWorkspacePrefill = 1;
 constexpr int kWorkspaceSlots = 2;
 void* device_workspace(int device, size_t bytes, int slot);
 
+// Compute units of `device` (cached; 256 on MI355X), 0 if the query fails.
+int device_cu_count(int device);
+
 // Optional pair of events recorded on the launch stream immediately before and
 // after the dominant kernel of the next entry-point call (benchmarks time that
 // kernel on its own stream with them).  Cleared after use.

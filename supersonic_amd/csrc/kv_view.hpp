@@ -31,6 +31,20 @@ struct KvView {
         }
         return b * seq_stride + h * head_stride + static_cast<int64_t>(t) * D;
     }
+    // row() for a wave-uniform (b, h, t): the block-table entry comes through
+    // the scalar cache (the table is read-only while a kernel runs), so the
+    // load is counted by lgkmcnt and waiting for it never drains the wave's
+    // outstanding vector loads.
+    __device__ __forceinline__ int64_t row_uniform(int b, int h, int t, int D) const {
+        if (bt) {
+            typedef const __attribute__((address_space(4))) int32_t* cptr;
+            const cptr cbt = reinterpret_cast<cptr>(reinterpret_cast<uintptr_t>(bt));
+            const int pg = cbt[static_cast<int64_t>(b) * max_pages + t / page_size];
+            return static_cast<int64_t>(pg) * page_stride + h * head_stride +
+                   static_cast<int64_t>(t % page_size) * D;
+        }
+        return b * seq_stride + h * head_stride + static_cast<int64_t>(t) * D;
+    }
     // Offset of token t's fp8 scale.
     __device__ __forceinline__ int64_t srow(int b, int h, int t) const {
         if (bt) {

@@ -25,6 +25,8 @@
 //   first, the heads of one kv head on one XCD.
 #include <cstdlib>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "kv_view.hpp"
 
@@ -41,6 +43,8 @@ struct PrefillParams {
     int Hq, Hkv, G, S, L, off;
     float scale_log2;
     int nqt;             // query tiles of 128 rows
+    int B;               // sequences
+    int n_wg;            // workgroups of the persistent grid
     // drop-in output: f32, element (b, h, row, d) at b*o_bs + h*o_hs + row*o_rs + d
     float* out_f32;
     int64_t o_bs, o_hs, o_rs;
@@ -211,14 +215,14 @@ __device__ unsigned long long g_prefill_trace[16 * 2 * 64 * 6];
     } while (0)
 // Workgroup timeline: s_memrealtime at entry (slot 0), after the query
 // prologue (1), after the key loop (2) and at exit (3), the hardware id (4),
-// the tile count (5), after the query norm (6) and after the query RoPE (7).
+// the tile count (5), (XCC_ID << 32 | HW_ID in 4), after the query norm (6) and after the query RoPE (7).
 __device__ unsigned long long g_prefill_wg[4096 * 8];
 #define SSA_WG_STAMP(slot)                                                                          \
     do {                                                                                            \
-        if (tid == 0 && blockIdx.x < 4096) {                                                        \
-            g_prefill_wg[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memrealtime();               \
-            if ((slot) == 0) g_prefill_wg[blockIdx.x * 8 + 4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)); \
-            if ((slot) == 0) g_prefill_wg[blockIdx.x * 8 + 5] = ntiles;                            \
+        if (tid == 0 && (qt * p.Hq + h) * p.B + b < 4096) {                                                        \
+            g_prefill_wg[((qt * p.Hq + h) * p.B + b) * 8 + (slot)] = __builtin_amdgcn_s_memrealtime();               \
+            if ((slot) == 0) g_prefill_wg[((qt * p.Hq + h) * p.B + b) * 8 + 4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)) | (static_cast<unsigned long long>(__builtin_amdgcn_s_getreg(20 | (15 << 11))) << 32); \
+            if ((slot) == 0) g_prefill_wg[((qt * p.Hq + h) * p.B + b) * 8 + 5] = ntiles;                            \
         }                                                                                           \
     } while (0)
 #else
@@ -254,26 +258,32 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     // [stage][K | V] tiles; stage 0 also holds the query rows in the prologue
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * T::STAGE];
 
-    // Work item, XCD-aware (workgroup i runs on XCD i % 8): the heads sharing a
-    // kv head run on one XCD, whose L2 keeps that kv head's K/V; query tiles run
-    // longest first.
-    int qt, h;
-    {
-        const int bid = blockIdx.x;
-        const int hpx = p.Hq / 8;
-        if (hpx > 0 && (p.Hq % 8) == 0) {
-            const int xcd = bid & 7, slot = bid >> 3;
-            qt = p.nqt - 1 - slot / hpx;
-            h = xcd * hpx + slot % hpx;
-        } else {
-            qt = p.nqt - 1 - bid / p.Hq;
-            h = bid % p.Hq;
-        }
-    }
-    const int b = blockIdx.y;
-    const int kvh = h / p.G;
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy offsets stay in SGPRs
+    // Persistent grid (one workgroup per CU), items longest first.  When the
+    // heads split evenly over the 8 XCDs (workgroup i runs on XCD i % 8), each
+    // XCD has its own item list holding the heads that share its kv heads, so
+    // its L2 keeps their K/V.  Workgroup j of a list of W takes items j,
+    // 2W-1-j, 2W+j, ...: a long item pairs with a short one and every
+    // workgroup gets about the same number of key tiles.
+    const int bid = blockIdx.x;
+    const int hpx = p.Hq / 8;
+    const bool by_xcd = hpx > 0 && (p.Hq % 8) == 0 && (p.n_wg % 8) == 0;
+    const int j = by_xcd ? (bid >> 3) : bid;
+    const int W = by_xcd ? (p.n_wg >> 3) : p.n_wg;
+    const int hpi = by_xcd ? hpx : p.Hq;     // heads per item list
+    const int n_items = p.nqt * hpi * p.B;
+    // One work item = 128 query rows of one head of one sequence, run by the
+    // copy waves (COPY) or the compute waves.  A `return` inside ends the
+    // item, not the workgroup.
+    auto run_item = [&](auto copy_tag, const int qt, const int h, const int b) {
+        constexpr bool COPY = decltype(copy_tag)::value;
+    // Opaque per item, so the compiler does not hoist lane-derived values and
+    // loads (norm weights, offsets) out of the item loop, where they would
+    // stay live through the key loop.
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
+    const int kvh = h / p.G;
     const int g4 = lane >> 4;
     const int q0 = qt * 128;
     const int row_w0 = q0 + 16 * wave;
@@ -298,11 +308,12 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const int vt_lane0 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (lane >> 4));
     const int vt_lane1 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (4 + (lane >> 4)));
     const uint16_t* vt_head = p.vt + (static_cast<int64_t>(b) * p.Hkv + kvh) * D * p.vt_ld;
-    auto issue_tile = [&](int it, int st) {
+    // Tile it goes to stage (it + 1) & 1.
+    auto issue_tile = [&](int it) {
         const int k0 = it * 64;
-        const int64_t base = p.kv.row(b, kvh, k0, D) * 2;  // a tile lies inside one page
-        const int bytes = min(64, L - k0) * T::ROWB;
-        const __amdgpu_buffer_rsrc_t kr = tile_rsrc(p.kv.k + base, bytes);
+        const int st = (it + 1) & 1;
+        const int64_t base = p.kv.row_uniform(b, kvh, k0, D) * 2;  // a tile lies inside one page
+        const __amdgpu_buffer_rsrc_t kr = tile_rsrc(p.kv.k + base, min(64, L - k0) * T::ROWB);
         const __amdgpu_buffer_rsrc_t vr = tile_rsrc(reinterpret_cast<const uint8_t*>(vt_head + k0),
                                                     D * vt_rowb - 2 * k0);
         const int cw = wave - kPrefillWaves;
@@ -318,20 +329,23 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         }
     };
     SSA_WG_STAMP(0);
-    if (wave >= kPrefillWaves) {
-        // Copy waves: tile it goes to stage (it + 1) & 1; the next tile is
-        // issued once everyone has passed the barrier of tile it (its stage's
-        // previous tile has been read).  Same barrier count as the compute
+    if constexpr (COPY) {
+        // Copy waves: the next tile is issued once everyone has passed the
+        // barrier of tile it (its stage's previous tile has been read) and has
+        // landed by the next barrier.  Same barrier count as the compute
         // waves; the stage-0 query staging of the fused prologue is finished
         // before the first barrier.
-        if (ntiles > 0) issue_tile(0, 1);
+        if (ntiles > 0) issue_tile(0);
         for (int it = 0; it < ntiles; ++it) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (it + 1 < ntiles) issue_tile(it + 1, it & 1);
+            if (it + 1 < ntiles) issue_tile(it + 1);
         }
+        // item end: both stages are free once every wave has passed it, so the
+        // next item's first tile goes out during the compute waves' epilogue
+        __syncthreads();
         return;
-    }
+    } else {
 
     // ------------------------------------------------ Q^T operand (registers)
     // B operand of S^T = K Q^T: lane holds query row (lane & 15), dims 32 s + 8 g4 + j.
@@ -564,6 +578,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         SSA_STAMP(4);
     }
 
+    __syncthreads();                    // item end (the copy waves' last barrier)
     SSA_WG_STAMP(2);
     // ------------------------------------------------ epilogue
     // O^T C layout: lane holds row myrow, dims 16 d + 4 g4 + i.
@@ -605,6 +620,26 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         }
     }
     SSA_WG_STAMP(3);
+    }  // compute waves
+    };
+
+    // Separate loops for the copy and the compute waves (same items, same
+    // barrier count per item), so neither keeps the other's registers live.
+    // The next item is read after the item-end barrier of the current one.
+    auto for_items = [&](auto copy_tag) {
+        for (int r = 0;; ++r) {
+            const int m = (r & 1) ? (r + 1) * W - 1 - j : r * W + j;
+            if (m >= n_items) break;          // the sequence of m is increasing
+            const int qt = p.nqt - 1 - m / (hpi * p.B);
+            const int rem = m % (hpi * p.B);
+            const int h = (by_xcd ? (bid & 7) * hpx : 0) + rem % hpi;
+            run_item(copy_tag, qt, h, rem / hpi);
+        }
+    };
+    if (wave >= kPrefillWaves)
+        for_items(std::true_type{});
+    else
+        for_items(std::false_type{});
 #endif
 }
 
@@ -804,8 +839,17 @@ static hipError_t stage_vt(int device, hipStream_t st, const KvView& kv, int B, 
 // ----------------------------------------------------------------------------
 // Host side
 // ----------------------------------------------------------------------------
+// Persistent grid: one workgroup per CU (a workgroup's LDS allows no second
+// one), a multiple of 8 so the XCD-aware item lists stay aligned, and never
+// more workgroups than items.
 template <typename QT, bool FUSED>
-static hipError_t launch_prefill(int D, dim3 grid, hipStream_t st, const PrefillParams& p) {
+static hipError_t launch_prefill(int device, int D, hipStream_t st, PrefillParams& p) {
+    const int items = p.nqt * p.Hq * p.B;
+    int n = device_cu_count(device);
+    if (n <= 0) n = 256;
+    n = n >= 8 ? n & ~7 : n;
+    p.n_wg = items < n ? items : n;
+    const dim3 grid(static_cast<unsigned>(p.n_wg));
     switch (D) {
     case 64: hipLaunchKernelGGL((prefill_kernel<QT, 64, FUSED>), grid, dim3(kPrefillThreads), 0, st, p); break;
     case 128: hipLaunchKernelGGL((prefill_kernel<QT, 128, FUSED>), grid, dim3(kPrefillThreads), 0, st, p); break;
@@ -862,12 +906,13 @@ static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t 
     p.o_rs = p.q_rs;
     p.o_hs = p.q_hs;
     p.o_bs = p.q_bs;
-    dim3 grid(p.nqt * static_cast<unsigned>(Hq), static_cast<unsigned>(B));
+    p.B = static_cast<int>(B);
     if (kv_len > 0 && stage_vt(static_cast<int>(device), nullptr, p.kv, static_cast<int>(B), static_cast<int>(Hkv),
                                static_cast<int>(kv_len), static_cast<int>(D), p) != hipSuccess)
         return 11;
-    const hipError_t e = dtype == 0 ? launch_prefill<f16_t, false>(static_cast<int>(D), grid, nullptr, p)
-                                    : launch_prefill<bf16_t, false>(static_cast<int>(D), grid, nullptr, p);
+    const int dev = static_cast<int>(device);
+    const hipError_t e = dtype == 0 ? launch_prefill<f16_t, false>(dev, static_cast<int>(D), nullptr, p)
+                                    : launch_prefill<bf16_t, false>(dev, static_cast<int>(D), nullptr, p);
     if (e != hipSuccess) return 11;
     if (hipDeviceSynchronize() != hipSuccess) return 12;
     return 0;
@@ -960,12 +1005,12 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.sin_t = static_cast<const uint16_t*>(sin_table);
     p.half_rot = static_cast<int>(rotary_dim / 2);
     p.eps = eps;
-    dim3 grid(p.nqt * static_cast<unsigned>(q_heads), 1);
+    p.B = 1;
     if (stage_vt(static_cast<int>(device_ordinal), st, kv, 1, p.Hkv, p.L, static_cast<int>(head_dim), p) != hipSuccess)
         return SUPERSONIC_ERR_LAUNCH;
     const ProfileEvents prof = take_profile_events();
     if (prof.before) (void)hipEventRecord(prof.before, st);
-    if (launch_prefill<bf16_t, true>(static_cast<int>(head_dim), grid, st, p) != hipSuccess)
+    if (launch_prefill<bf16_t, true>(static_cast<int>(device_ordinal), static_cast<int>(head_dim), st, p) != hipSuccess)
         return SUPERSONIC_ERR_LAUNCH;
     if (prof.after) (void)hipEventRecord(prof.after, st);
     return 0;

@@ -47,6 +47,20 @@ void* device_workspace(int device, size_t bytes, int slot) {
     return w.ptr;
 }
 
+int device_cu_count(int device) {
+    static std::mutex m;
+    static std::vector<int> counts;
+    std::lock_guard<std::mutex> lock(m);
+    if (device < 0) return 0;
+    if (static_cast<size_t>(device) >= counts.size()) counts.resize(device + 1, -1);
+    if (counts[device] < 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) n = 0;
+        counts[device] = n;
+    }
+    return counts[device];
+}
+
 namespace {
 std::mutex g_prof_mutex;
 ProfileEvents g_prof;
