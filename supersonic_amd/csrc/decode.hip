@@ -33,6 +33,7 @@
 //           (or fp8 codes + scales) into the cache and, after its cached
 //           blocks, processes the new token as a one-token block read from LDS,
 //           unquantised (as full_attention_4b.hip:5351-5353 does).
+#include <algorithm>
 #include <cstdlib>
 #include <mutex>
 #include <utility>
@@ -51,6 +52,11 @@ struct DecodeParams {
     const int32_t* lens;      // kv_lens [B] (attend) or positions [B] (fused)
     int len_plus;             // 0 (attend) or 1 (fused: len = position + 1)
     int Hq, Hkv, G, chunk, nsplit;
+    // Ragged plan (ragged != 0): the workgroups of a 1-D grid split the batch's
+    // total length into chunks of about total * Hkv / target tokens, so every
+    // workgroup gets about the same number of tokens whatever the lengths;
+    // chunk and nsplit are then unused.
+    int ragged, B, target, min_chunk;
     float scale_log2;         // softmax scale * log2(e)
     int fused;
     const uint16_t* k_new;    // [B, Hkv*D] bf16
@@ -61,8 +67,8 @@ struct DecodeParams {
     const uint16_t* sin_t;
     int half_rot;
     float eps;
-    float* part_o;            // [B, Hq, nsplit, D]
-    float* part_ml;           // [B, Hq, nsplit, 2] (max in log2 units, sum)
+    float* part_o;            // [rows, D], row of (b, h, split) = pre_b * Hq + h * n_b + split
+    float* part_ml;           // [rows, 2] (max in log2 units, sum)
     unsigned* arrivals;       // [B, Hkv] split arrival counters, zero between calls
     const uint16_t* gate;     // NULL, or gate element (b, h, d) at b*g_bstride + h*g_hstride + d
     int64_t g_bstride, g_hstride;
@@ -180,10 +186,91 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     __shared__ float ml_s[NW][GP][2];
     __shared__ int next_blk;                   // next 16-token block to claim
 
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Work item (b, kv head, split), chunk length, and the partial rows of
+    // sequence b: pre_b splits before it, n_b of its own per head.
+    int split, kvh, b, chunk, n_b;
+    int64_t pre_b;
+    if (p.ragged) {
+        // Every workgroup plans the same way from the lengths: chunk =
+        // ceil(total * Hkv / target) rounded up to 64 (at least min_chunk),
+        // sequence b gets n_b = max(1, ceil(len_b / chunk)) splits per kv
+        // head, items are ordered (b, kv head, split), and workgroup i takes
+        // item i (past the last item it has nothing to do).
+        __shared__ int plan_s[6];
+        if (wave == 0) {
+            int64_t tot = 0;
+            for (int b0 = 0; b0 < p.B; b0 += 64) {
+                const int bi = b0 + lane;
+                tot += bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
+            }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) tot += __shfl_xor(tot, o);
+            // Per-sequence rounding can push the item count past the target
+            // (a second, mostly idle round): grow the chunk in proportion
+            // until the items fit (a few passes; uniform lengths need none).
+            int64_t c = (tot * p.Hkv + p.target - 1) / p.target;
+            c = max((c + 63) / 64 * 64, static_cast<int64_t>(p.min_chunk));
+            for (int pass = 0; pass < 4; ++pass) {
+                int64_t items = 0;
+                for (int b0 = 0; b0 < p.B; b0 += 64) {
+                    const int bi = b0 + lane;
+                    const int64_t l = bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
+                    items += bi < p.B ? max(static_cast<int64_t>(1), (l + c - 1) / c) : 0;
+                }
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) items += __shfl_xor(items, o);
+                items *= p.Hkv;
+                if (items <= p.target) break;
+                c = (c * items + p.target - 1) / p.target;
+                c = (c + 63) / 64 * 64;
+            }
+            const int ch = static_cast<int>(c);
+            if (lane == 0) plan_s[0] = -1;
+            const int w = blockIdx.x;
+            int run = 0, run_n = 0;  // items and splits of the sequences before b0
+            for (int b0 = 0; b0 < p.B; b0 += 64) {
+                const int bi = b0 + lane;
+                const int l = bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
+                const int n = bi < p.B ? max(1, (l + ch - 1) / ch) : 0;
+                int incl = n;        // inclusive scan of the split counts
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int t = __shfl_up(incl, o);
+                    if (lane >= o) incl += t;
+                }
+                const int first = run + (incl - n) * p.Hkv;  // first item of sequence bi
+                if (bi < p.B && w >= first && w < first + n * p.Hkv) {
+                    plan_s[0] = bi;
+                    plan_s[1] = (w - first) / n;
+                    plan_s[2] = (w - first) % n;
+                    plan_s[3] = n;
+                    plan_s[4] = run_n + incl - n;
+                }
+                const int tot_n = __shfl(incl, 63);
+                run += tot_n * p.Hkv;
+                run_n += tot_n;
+            }
+            if (lane == 0) plan_s[5] = ch;
+        }
+        __syncthreads();
+        b = plan_s[0];
+        if (b < 0) return;  // uniform
+        kvh = plan_s[1];
+        split = plan_s[2];
+        n_b = plan_s[3];
+        pre_b = plan_s[4];
+        chunk = plan_s[5];
+    } else {
+        split = blockIdx.x;
+        kvh = blockIdx.y;
+        b = blockIdx.z;
+        chunk = p.chunk;
+        n_b = p.nsplit;
+        pre_b = static_cast<int64_t>(b) * p.nsplit;
+    }
     const int len = p.lens[b] + p.len_plus;
-    const int t_begin = split * p.chunk;
+    const int t_begin = split * chunk;
     if (t_begin >= len) {  // uniform: ragged batch, nothing to do
         if (len <= 0 && split == 0) {
             // No tokens at all: the output is zero (what the merge of no splits gives).
@@ -194,7 +281,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         }
         return;
     }
-    const int t_end = min(len, t_begin + p.chunk);
+    const int t_end = min(len, t_begin + chunk);
     const int G = p.G;
     const int pos = len - 1;
     const bool owner = p.fused && pos >= t_begin && pos < t_end;
@@ -574,7 +661,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         float o = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) o += smem[(w * GP + h) * D + d];
-        const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
+        const int64_t row = pre_b * p.Hq + static_cast<int64_t>(kvh * G + h) * n_b + split;
         store_agent(p.part_o + row * D + d, o);
     }
     if (wave == 0) {
@@ -586,7 +673,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
             float L = 0.f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) L += exp2f(ml_s[w][h][0] - M) * ml_s[w][h][1];
-            const int64_t row = (static_cast<int64_t>(b) * p.Hq + kvh * G + h) * p.nsplit + split;
+            const int64_t row = pre_b * p.Hq + static_cast<int64_t>(kvh * G + h) * n_b + split;
             store_agent(&p.part_ml[2 * row], M);
             store_agent(&p.part_ml[2 * row + 1], L);
         }
@@ -600,7 +687,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     // before it arrives, so no device-wide fence (an L2 writeback and
     // invalidate on this GPU) is needed.
     __shared__ int last_s;
-    const int ns = (len + p.chunk - 1) / p.chunk;
+    const int ns = (len + chunk - 1) / chunk;  // splits that hold tokens (<= n_b)
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
     __syncthreads();
     if (tid == 0) {
@@ -612,7 +699,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     if (!last_s) return;
     for (int hh = wave; hh < G; hh += NW) {
         const int h = kvh * G + hh;
-        const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + h) * p.nsplit;
+        const int64_t row0 = pre_b * p.Hq + static_cast<int64_t>(h) * n_b;
         // One online pass over the splits, MCH at a time with all their loads
         // in flight together (a handful of round trips instead of one per split).
         constexpr int DPL = D / 64;  // dims per lane
@@ -680,10 +767,17 @@ static int env_int(const char* name, int dflt) {
 
 // Chunk of tokens per workgroup: enough workgroups to fill 256 CUs a few
 // times over, but chunks of at least 64 tokens (4 waves x 16).
-static SplitPlan plan_splits(int B, int Hkv, int max_len, int waves) {
+static int decode_target(int waves) {
     // 2048 resident waves: one 8-wave or two 4-wave workgroups per CU
-    const int target = env_int("SUPERSONIC_DECODE_TARGET_WGS", 2048 / waves);
-    const int min_chunk = env_int("SUPERSONIC_DECODE_MIN_CHUNK", 128);
+    return std::max(1, env_int("SUPERSONIC_DECODE_TARGET_WGS", 2048 / waves));
+}
+static int decode_min_chunk() { return std::max(64, env_int("SUPERSONIC_DECODE_MIN_CHUNK", 128)); }
+
+// Uniform plan (one length for the whole batch): the same split count for
+// every sequence.
+static SplitPlan plan_splits(int B, int Hkv, int max_len, int waves) {
+    const int target = decode_target(waves);
+    const int min_chunk = decode_min_chunk();
     const int pairs = B * Hkv;
     int want = (target + pairs - 1) / pairs;
     if (want < 1) want = 1;
@@ -691,12 +785,20 @@ static SplitPlan plan_splits(int B, int Hkv, int max_len, int waves) {
     chunk = ((chunk + 63) / 64) * 64;
     if (chunk < min_chunk) chunk = min_chunk;
     int nsplit = (max_len + chunk - 1) / chunk;
-    if (nsplit > 1024) {  // the merge kernel stages at most 1024 split weights
-        chunk = ((max_len + 1023) / 1024 + 63) / 64 * 64;
-        nsplit = (max_len + chunk - 1) / chunk;
-    }
     if (nsplit < 1) nsplit = 1;
     return {chunk, nsplit};
+}
+
+// Partial rows of a call: the uniform plan needs B * Hq * nsplit; the ragged
+// plan at most (ceil(target / Hkv) + B) * Hq (sum over b of ceil(len_b /
+// chunk) <= total / chunk + B, and chunk >= total * Hkv / target).  Sized for
+// the larger so that either plan fits.
+static size_t decode_rows(int B, int Hq, int Hkv, int max_len, int waves) {
+    const SplitPlan sp = plan_splits(B, Hkv, max_len, waves);
+    const size_t uni = static_cast<size_t>(B) * Hq * sp.nsplit;
+    const int target = decode_target(waves);
+    const size_t rag = (static_cast<size_t>((target + Hkv - 1) / Hkv) + B) * Hq;
+    return std::max(uni, rag);
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -708,8 +810,7 @@ static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 constexpr size_t kArrivalBytes = 64 * 1024;
 constexpr int kMaxArrivals = static_cast<int>(kArrivalBytes / sizeof(unsigned));
 
-static size_t workspace_bytes_for(int B, int Hq, int D, int nsplit) {
-    const size_t rows = static_cast<size_t>(B) * Hq * nsplit;
+static size_t workspace_bytes_for(size_t rows, int D) {
     return kArrivalBytes + align256(rows * D * sizeof(float)) + align256(rows * 2 * sizeof(float));
 }
 
@@ -747,6 +848,7 @@ struct DecodeRequest {
     size_t workspace_bytes;
     int device;
     hipStream_t stream;
+    bool ragged;      // per-sequence lengths: plan on the device from the lengths
 };
 
 // Returns 0, or a SUPERSONIC_ERR_* status.
@@ -759,8 +861,10 @@ static int run_decode(DecodeRequest& r) {
     if (r.B <= 0) return 0;
     if (static_cast<int64_t>(r.B) * r.Hkv > kMaxArrivals) return SUPERSONIC_ERR_RANGE;
     if (r.max_len <= 0) r.max_len = 1;
-    const SplitPlan sp = plan_splits(r.B, r.Hkv, r.max_len, decode_waves(GP));
-    const size_t need = workspace_bytes_for(r.B, r.Hq, r.D, sp.nsplit);
+    const int waves = decode_waves(GP);
+    const SplitPlan sp = plan_splits(r.B, r.Hkv, r.max_len, waves);
+    const size_t rows = decode_rows(r.B, r.Hq, r.Hkv, r.max_len, waves);
+    const size_t need = workspace_bytes_for(rows, r.D);
     void* ws = r.workspace;
     if (ws) {
         if (r.workspace_bytes < need) return SUPERSONIC_ERR_WORKSPACE;
@@ -768,13 +872,16 @@ static int run_decode(DecodeRequest& r) {
         ws = device_workspace(r.device, need, kWorkspaceDecode);
         if (!ws) return SUPERSONIC_ERR_WORKSPACE;
     }
-    const size_t rows = static_cast<size_t>(r.B) * r.Hq * sp.nsplit;
     DecodeParams& p = r.prm;
     p.Hq = r.Hq;
     p.Hkv = r.Hkv;
     p.G = G;
     p.chunk = sp.chunk;
     p.nsplit = sp.nsplit;
+    p.ragged = r.ragged ? 1 : 0;
+    p.B = r.B;
+    p.target = decode_target(waves);
+    p.min_chunk = decode_min_chunk();
     p.scale_log2 = r.scale * kLog2e;
     p.arrivals = static_cast<unsigned*>(ws);
     p.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes);
@@ -784,7 +891,9 @@ static int run_decode(DecodeRequest& r) {
     p.g_hstride = r.g_hstride;
     p.out = r.out;
 
-    dim3 grid(sp.nsplit, r.Hkv, r.B);
+    // ragged: one workgroup per item, at most target + B * Hkv items
+    const dim3 grid = r.ragged ? dim3(static_cast<unsigned>(p.target + r.B * r.Hkv), 1, 1)
+                               : dim3(sp.nsplit, r.Hkv, r.B);
     const ProfileEvents prof = take_profile_events();
     if (prof.before) (void)hipEventRecord(prof.before, r.stream);
     hipError_t e;
@@ -902,10 +1011,9 @@ extern "C" size_t supersonic_attn_gfx950_decode_workspace_size(
     if (kv_heads == 0) return 0;
     const size_t G = q_heads / kv_heads;
     const int GP = G <= 4 ? 4 : (G <= 8 ? 8 : 16);
-    const SplitPlan sp = plan_splits(static_cast<int>(batch), static_cast<int>(kv_heads),
-                                     max_kv_len ? static_cast<int>(max_kv_len) : 1, decode_waves(GP));
-    return workspace_bytes_for(static_cast<int>(batch), static_cast<int>(q_heads), static_cast<int>(head_dim),
-                               sp.nsplit);
+    const size_t rows = decode_rows(static_cast<int>(batch), static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                                    max_kv_len ? static_cast<int>(max_kv_len) : 1, decode_waves(GP));
+    return workspace_bytes_for(rows, static_cast<int>(head_dim));
 }
 
 static int check_sizes(size_t a, size_t b, size_t c, size_t d, size_t e) {
@@ -938,6 +1046,7 @@ extern "C" int supersonic_attn_gfx950_decode(
     r.Hkv = static_cast<int>(kv_heads);
     r.D = static_cast<int>(head_dim);
     r.max_len = static_cast<int>(max_kv_len);
+    r.ragged = true;
     r.scale = scale;
     r.device = static_cast<int>(device_ordinal);
     r.stream = static_cast<hipStream_t>(stream);
@@ -985,6 +1094,7 @@ extern "C" int supersonic_attn_gfx950_decode_attend(
     r.Hkv = static_cast<int>(kv_heads);
     r.D = static_cast<int>(head_dim);
     r.max_len = static_cast<int>(max_kv_len);
+    r.ragged = true;
     r.scale = scale;
     r.device = static_cast<int>(device_ordinal);
     r.stream = static_cast<hipStream_t>(stream);
