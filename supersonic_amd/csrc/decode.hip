@@ -195,8 +195,9 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         // Every workgroup plans the same way from the lengths: chunk =
         // ceil(total * Hkv / target) rounded up to 64 (at least min_chunk),
         // sequence b gets n_b = max(1, ceil(len_b / chunk)) splits per kv
-        // head, items are ordered (b, kv head, split), and workgroup i takes
-        // item i (past the last item it has nothing to do).
+        // head, each of them ceil(len_b / n_b) tokens (rounded up to 16), items
+        // are ordered (b, kv head, split), and workgroup i takes item i (past
+        // the last item it has nothing to do).
         __shared__ int plan_s[6];
         if (wave == 0) {
             int64_t tot = 0;
@@ -246,12 +247,14 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
                     plan_s[2] = (w - first) % n;
                     plan_s[3] = n;
                     plan_s[4] = run_n + incl - n;
+                    // the sequence's n splits share its length equally (16-token
+                    // blocks), so no split is left with a short remainder
+                    plan_s[5] = l > 0 ? ((l + n - 1) / n + 15) / 16 * 16 : ch;
                 }
                 const int tot_n = __shfl(incl, 63);
                 run += tot_n * p.Hkv;
                 run_n += tot_n;
             }
-            if (lane == 0) plan_s[5] = ch;
         }
         __syncthreads();
         b = plan_s[0];
@@ -436,7 +439,8 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
 
     // Block data of one 16-token block, loaded one block ahead (registers).
     struct Blk {
-        op_t kb[KSTEPS];
+        op_t kb[FP8 ? 1 : KSTEPS];
+        u32x2_v kr8[FP8 ? KSTEPS : 1];   // raw e4m3 K: converted when the block is processed
         u32x4_v vr16[FP8 ? 1 : VINS];
         u32x2_v vr8[FP8 ? VINS : 1];
         float ksc, vsc;
@@ -462,7 +466,8 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
             if constexpr (!FP8) {
                 B.kb[s] = as_op<op_t>(__builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * s, 0, kStream)));
             } else {
-                B.kb[s] = as_op<op_t>(fp8x8_to_bf16x8(__builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane_off + 32 * s, 0, kStream))));
+                // raw bytes only: converted when the block is processed
+                B.kr8[s] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane_off + 32 * s, 0, kStream));
             }
         }
         // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
@@ -545,9 +550,12 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     auto process_blk = [&](int blk, Blk& B) {
 #ifdef SSA_DECODE_NOCOMPUTE
         {
-            u32x4_v x = __builtin_bit_cast(u32x4_v, B.kb[0]);
+            u32x4_v x = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int s = 1; s < KSTEPS; ++s) x ^= __builtin_bit_cast(u32x4_v, B.kb[s]);
+            for (int s = 0; s < KSTEPS; ++s) {
+                if constexpr (!FP8) x ^= __builtin_bit_cast(u32x4_v, B.kb[s]);
+                else x[s & 3] ^= B.kr8[s][0] ^ B.kr8[s][1];
+            }
             if constexpr (!FP8) {
 #pragma unroll
                 for (int j = 0; j < VINS; ++j) x ^= B.vr16[j];
@@ -557,10 +565,18 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         }
 #endif
         const int t0 = t_begin + blk * 16;
-        process(min(16, t_main - t0), B.kb, B.ksc, B.vsc, [&](int j, float (&vf)[8]) {
+        auto vdec = [&](int j, float (&vf)[8]) {
             if constexpr (!FP8) unpack8<QT>(B.vr16[j], vf);
             else fp8x8_to_f32(B.vr8[j], vf);
-        });
+        };
+        if constexpr (!FP8) {
+            process(min(16, t_main - t0), B.kb, B.ksc, B.vsc, vdec);
+        } else {
+            op_t kb[KSTEPS];
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) kb[s] = as_op<op_t>(fp8x8_to_bf16x8(B.kr8[s]));
+            process(min(16, t_main - t0), kb, B.ksc, B.vsc, vdec);
+        }
     };
 
     // Software pipeline: the next block's loads are in flight while the
