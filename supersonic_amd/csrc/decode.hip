@@ -96,15 +96,15 @@ __device__ __forceinline__ OP as_op(const u32x4_v& w) {
     return r;
 }
 
-// 8 e4m3 bytes -> 8 bf16 (exact: every e4m3 value is a bf16 value).
+// 8 e4m3 bytes -> 8 bf16 (exact: every e4m3 value is a bf16 value), two
+// bytes per gfx950 v_cvt_scalef32_pk_bf16_fp8 at scale 1.
 __device__ __forceinline__ u32x4_v fp8x8_to_bf16x8(u32x2_v w) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     u32x4_v r;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        f32x2_v lo = fp8x2_to_f32(w[i], false);
-        f32x2_v hi = fp8x2_to_f32(w[i], true);
-        r[2 * i] = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u);
-        r[2 * i + 1] = __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u);
+        r[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, false));
+        r[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, true));
     }
     return r;
 }
@@ -520,10 +520,18 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+        // Rescale only when some head's running max moved (alpha != 1; the
+        // factors are wave-uniform, so this is a scalar branch): after the
+        // first blocks the max rarely changes.
+        bool moved = false;
 #pragma unroll
-        for (int h = 0; h < GP; ++h)
+        for (int h = 0; h < GP; ++h) moved |= alpha[h] != 1.0f;
+        if (moved) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
+            for (int h = 0; h < GP; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
+        }
 
 #pragma unroll
         for (int j = 0; j < VINS; ++j) {
