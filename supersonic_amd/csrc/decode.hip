@@ -193,7 +193,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     int64_t pre_b;
     if (p.ragged) {
         // Every workgroup plans the same way from the lengths: chunk =
-        // ceil(total * Hkv / target) rounded up to 64 (at least min_chunk),
+        // ceil(total * Hkv / target) rounded up to 16 (at least min_chunk),
         // sequence b gets n_b = max(1, ceil(len_b / chunk)) splits per kv
         // head, each of them ceil(len_b / n_b) tokens (rounded up to 16), items
         // are ordered (b, kv head, split), and workgroup i takes item i (past
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
             // (a second, mostly idle round): grow the chunk in proportion
             // until the items fit (a few passes; uniform lengths need none).
             int64_t c = (tot * p.Hkv + p.target - 1) / p.target;
-            c = max((c + 63) / 64 * 64, static_cast<int64_t>(p.min_chunk));
+            c = max((c + 15) / 16 * 16, static_cast<int64_t>(p.min_chunk));
             for (int pass = 0; pass < 4; ++pass) {
                 int64_t items = 0;
                 for (int b0 = 0; b0 < p.B; b0 += 64) {
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
                 items *= p.Hkv;
                 if (items <= p.target) break;
                 c = (c * items + p.target - 1) / p.target;
-                c = (c + 63) / 64 * 64;
+                c = (c + 15) / 16 * 16;
             }
             const int ch = static_cast<int>(c);
             if (lane == 0) plan_s[0] = -1;
