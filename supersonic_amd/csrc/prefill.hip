@@ -689,96 +689,6 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(const float* q, const 
 }
 
 // ----------------------------------------------------------------------------
-// Fused prefill: K RMSNorm + RoPE and the cache write for the chunk's tokens.
-// One wave per (token, kv head); the row is staged in a per-wave LDS slot so
-// RoPE pairs (i, i + half_rot) can be any distance apart.
-// ----------------------------------------------------------------------------
-struct KvPrepParams {
-    const uint16_t* k_new;  // [S, Hkv*D]
-    const uint16_t* v_new;
-    const uint16_t* k_norm_w;
-    const uint16_t* cos_t;
-    const uint16_t* sin_t;
-    KvView kv;
-    int S, Hkv, D, off, half_rot, fp8;
-    float eps;
-};
-
-__global__ __launch_bounds__(256) void kv_prep_kernel(KvPrepParams p) {
-    __shared__ float rows_s[4][2][512];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + wave;
-    if (row >= p.S * p.Hkv) return;
-    const int s = row / p.Hkv, h = row % p.Hkv;
-    const int D = p.D;
-    float* kr = rows_s[wave][0];
-    float* vr = rows_s[wave][1];
-    const uint16_t* ksrc = p.k_new + static_cast<int64_t>(row) * D;
-    const uint16_t* vsrc = p.v_new + static_cast<int64_t>(row) * D;
-    float ss = 0.f;
-    for (int d = lane; d < D; d += 64) {
-        const float x = bf16_bits_to_f32(ksrc[d]);
-        kr[d] = x;
-        ss += x * x;
-        vr[d] = bf16_bits_to_f32(vsrc[d]);
-    }
-    ss = wave_sum(ss);
-    const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
-    for (int d = lane; d < D; d += 64) kr[d] = bf16_round(kr[d] * inv * (bf16_bits_to_f32(p.k_norm_w[d]) + 1.0f));
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int pos = p.off + s;
-    const int hr = p.half_rot;
-    float r0[4], r1[4];
-    int nr = 0;
-    for (int i = lane; i < hr; i += 64) {
-        const float c = bf16_bits_to_f32(p.cos_t[static_cast<int64_t>(pos) * hr + i]);
-        const float sn = bf16_bits_to_f32(p.sin_t[static_cast<int64_t>(pos) * hr + i]);
-        const float x0 = kr[i], x1 = kr[i + hr];
-        r0[nr] = bf16_round(x0 * c - x1 * sn);
-        r1[nr] = bf16_round(x0 * sn + x1 * c);
-        ++nr;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    nr = 0;
-    for (int i = lane; i < hr; i += 64) {
-        kr[i] = r0[nr];
-        kr[i + hr] = r1[nr];
-        ++nr;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int64_t o = p.kv.row(0, h, pos, D);
-    if (!p.fp8) {
-        uint16_t* kc = reinterpret_cast<uint16_t*>(p.kv.k) + o;
-        uint16_t* vc = reinterpret_cast<uint16_t*>(p.kv.v) + o;
-        for (int d = lane; d < D; d += 64) {
-            kc[d] = static_cast<uint16_t>(f32_to_bf16_bits(kr[d]));
-            vc[d] = static_cast<uint16_t>(f32_to_bf16_bits(vr[d]));
-        }
-    } else {
-        for (int which = 0; which < 2; ++which) {
-            const float* src = which ? vr : kr;
-            uint8_t* dst = (which ? p.kv.v : p.kv.k) + o;
-            float am = 0.f;
-            for (int d = lane; d < D; d += 64) am = fmaxf(am, fabsf(src[d]));
-            am = wave_max(am);
-            const float sc = fmaxf(am / 448.0f, 1e-12f);
-            const float iv = 1.0f / sc;
-            for (int d = lane * 4; d < D; d += 256) {
-                *reinterpret_cast<uint32_t*>(dst + d) =
-                    f32x4_to_fp8x4(src[d] * iv, src[d + 1] * iv, src[d + 2] * iv, src[d + 3] * iv);
-            }
-            if (lane == 0) (which ? p.kv.vs : p.kv.ks)[p.kv.srow(0, h, pos)] = sc;
-        }
-    }
-}
-
-// ----------------------------------------------------------------------------
 // V^T staging for the prefill kernel.  The PV product needs, per lane, 8
 // consecutive keys of one dim; the cache stores token rows.  This pass writes
 // each kv head's V transposed, dims as rows of vt_ld positions (kv_len rounded
@@ -812,6 +722,108 @@ __global__ __launch_bounds__(256) void vt_stage_kernel(KvView kv, uint16_t* vt, 
             w[j] = static_cast<uint32_t>(tile[vt_key_of_position(8 * c + 2 * j)][d]) |
                    (static_cast<uint32_t>(tile[vt_key_of_position(8 * c + 2 * j + 1)][d]) << 16);
         st16(dst + static_cast<int64_t>(d) * ld + 8 * c, w);
+    }
+}
+
+// Fused prefill, bf16 cache: one pass that appends the chunk's new tokens to
+// the cache and does vt_stage_kernel's work for every position.  One
+// workgroup per (64-position tile, kv head); lane c of a row holds dims
+// 8c .. 8c + 7 (16-byte accesses).  New tokens (position >= off): K gets
+// RMSNorm with (1 + w) and rotate-half RoPE (bf16 after each step, RoPE
+// partners read back through an LDS row), K and V go to the cache, and V to
+// the LDS tile; prefix positions read V back from the cache; the tile is then
+// written out transposed in the PV operand's key order.
+struct KvStageParams {
+    const uint16_t* k_new;  // [S, Hkv*D]
+    const uint16_t* v_new;
+    const uint16_t* k_norm_w;
+    const uint16_t* cos_t;
+    const uint16_t* sin_t;
+    KvView kv;
+    uint16_t* vt;           // [Hkv, D, ld]
+    int S, Hkv, off, L, ld, half_rot;
+    float eps;
+};
+
+constexpr int kKvStageWaves = 16;  // 4 per SIMD: the rows' memory round trips overlap
+
+template <int D>
+__global__ __launch_bounds__(64 * kKvStageWaves) void kv_stage_kernel(KvStageParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t vtile[64][D + 8];
+    constexpr int LPR = D / 8;          // lanes per row
+    constexpr int RPI = 64 / LPR;       // rows per wave instruction
+    __shared__ __attribute__((aligned(16))) uint16_t krow[kKvStageWaves][RPI][D];  // per-wave RoPE exchange
+    const int t0 = blockIdx.x * 64, h = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane % LPR;
+    const int hr = p.half_rot;
+    const bool rot = 8 * c < 2 * hr;
+    float wt[8];
+    unpack8<bf16_t>(ld16(p.k_norm_w + 8 * c), wt);
+    for (int r0 = wave * RPI; r0 < 64; r0 += kKvStageWaves * RPI) {
+        const int r = r0 + lane / LPR;
+        const int pos = t0 + r;
+        u32x4_v vw = {0u, 0u, 0u, 0u};
+        if (pos < p.L) {
+            const int64_t o = p.kv.row(0, h, pos, D) + 8 * c;
+            if (pos >= p.off) {
+                const int64_t src = (static_cast<int64_t>(pos - p.off) * p.Hkv + h) * D + 8 * c;
+                const u32x4_v kw = ld16(p.k_new + src);
+                vw = ld16(p.v_new + src);
+                u32x4_v cw4 = {0u, 0u, 0u, 0u}, sw4 = {0u, 0u, 0u, 0u};
+                if (rot) {
+                    const int64_t ti = static_cast<int64_t>(pos) * hr + (8 * c < hr ? 8 * c : 8 * c - hr);
+                    cw4 = ld16(p.cos_t + ti);
+                    sw4 = ld16(p.sin_t + ti);
+                }
+                float x[8];
+                unpack8<bf16_t>(kw, x);
+                float ss = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+                // the row's LPR lanes are aligned groups of the wave
+#pragma unroll
+                for (int m = 1; m < LPR; m <<= 1) ss += __shfl_xor(ss, m);
+                const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
+                u32x4_v nq;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    nq[e] = pk2<bf16_t>(x[2 * e] * inv * (wt[2 * e] + 1.0f), x[2 * e + 1] * inv * (wt[2 * e + 1] + 1.0f));
+                st16(&krow[wave][lane / LPR][8 * c], nq);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (rot) {
+                    const int pc = 8 * c < hr ? 8 * c + hr : 8 * c - hr;
+                    float xn[8], y[8], cs[8], sn[8];
+                    unpack8<bf16_t>(nq, xn);
+                    unpack8<bf16_t>(ld16(&krow[wave][lane / LPR][pc]), y);
+                    unpack8<bf16_t>(cw4, cs);
+                    unpack8<bf16_t>(sw4, sn);
+                    const float sg = 8 * c < hr ? -1.0f : 1.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        nq[e] = pk2<bf16_t>(xn[2 * e] * cs[2 * e] + sg * y[2 * e] * sn[2 * e],
+                                            xn[2 * e + 1] * cs[2 * e + 1] + sg * y[2 * e + 1] * sn[2 * e + 1]);
+                }
+                st16(reinterpret_cast<uint16_t*>(p.kv.k) + o, nq);
+                st16(reinterpret_cast<uint16_t*>(p.kv.v) + o, vw);
+            } else {
+                vw = ld16(reinterpret_cast<const uint16_t*>(p.kv.v) + o);
+            }
+        }
+        st16(&vtile[r][8 * c], vw);
+    }
+    __syncthreads();
+    uint16_t* dst = p.vt + static_cast<int64_t>(h) * D * p.ld + t0;
+    for (int idx = threadIdx.x; idx < D * 8; idx += 64 * kKvStageWaves) {
+        const int d = idx >> 3, cc = idx & 7;
+        u32x4_v w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = static_cast<uint32_t>(vtile[vt_key_of_position(8 * cc + 2 * j)][d]) |
+                   (static_cast<uint32_t>(vtile[vt_key_of_position(8 * cc + 2 * j + 1)][d]) << 16);
+        st16(dst + static_cast<int64_t>(d) * p.ld + 8 * cc, w);
     }
 }
 
@@ -966,22 +978,6 @@ extern "C" int supersonic_attn_gfx950_prefill(
     ScopedDevice scoped(static_cast<int>(device_ordinal));
     hipStream_t st = static_cast<hipStream_t>(stream);
 
-    KvPrepParams kp{};
-    kp.k_new = static_cast<const uint16_t*>(k_new);
-    kp.v_new = static_cast<const uint16_t*>(v_new);
-    kp.k_norm_w = static_cast<const uint16_t*>(k_norm_w);
-    kp.cos_t = static_cast<const uint16_t*>(cos_table);
-    kp.sin_t = static_cast<const uint16_t*>(sin_table);
-    kp.kv = kv;
-    kp.S = static_cast<int>(chunk_len);
-    kp.Hkv = static_cast<int>(kv_heads);
-    kp.D = static_cast<int>(head_dim);
-    kp.off = static_cast<int>(chunk_start);
-    kp.half_rot = static_cast<int>(rotary_dim / 2);
-    kp.fp8 = 0;
-    kp.eps = eps;
-    hipLaunchKernelGGL(kv_prep_kernel, dim3(grid1d(chunk_len * kv_heads, 4)), dim3(256), 0, st, kp);
-    if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
 
     PrefillParams p{};
     p.q = static_cast<const uint16_t*>(q_proj);
@@ -1006,8 +1002,38 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.half_rot = static_cast<int>(rotary_dim / 2);
     p.eps = eps;
     p.B = 1;
-    if (stage_vt(static_cast<int>(device_ordinal), st, kv, 1, p.Hkv, p.L, static_cast<int>(head_dim), p) != hipSuccess)
-        return SUPERSONIC_ERR_LAUNCH;
+    // K norm + RoPE + cache append for the chunk and the V^T staging of every
+    // position, in one pass
+    {
+        const int ld = (p.L + 63) / 64 * 64;
+        void* ws = device_workspace(static_cast<int>(device_ordinal),
+                                    static_cast<size_t>(p.Hkv) * head_dim * ld * 2, kWorkspacePrefill);
+        if (!ws) return SUPERSONIC_ERR_WORKSPACE;
+        p.vt = static_cast<const uint16_t*>(ws);
+        p.vt_ld = ld;
+        KvStageParams kp{};
+        kp.k_new = static_cast<const uint16_t*>(k_new);
+        kp.v_new = static_cast<const uint16_t*>(v_new);
+        kp.k_norm_w = static_cast<const uint16_t*>(k_norm_w);
+        kp.cos_t = static_cast<const uint16_t*>(cos_table);
+        kp.sin_t = static_cast<const uint16_t*>(sin_table);
+        kp.kv = kv;
+        kp.vt = static_cast<uint16_t*>(ws);
+        kp.S = static_cast<int>(chunk_len);
+        kp.Hkv = static_cast<int>(kv_heads);
+        kp.off = static_cast<int>(chunk_start);
+        kp.L = p.L;
+        kp.ld = ld;
+        kp.half_rot = static_cast<int>(rotary_dim / 2);
+        kp.eps = eps;
+        const dim3 grid(ld / 64, kp.Hkv);
+        switch (head_dim) {
+        case 64: hipLaunchKernelGGL(kv_stage_kernel<64>, grid, dim3(64 * kKvStageWaves), 0, st, kp); break;
+        case 128: hipLaunchKernelGGL(kv_stage_kernel<128>, grid, dim3(64 * kKvStageWaves), 0, st, kp); break;
+        default: hipLaunchKernelGGL(kv_stage_kernel<256>, grid, dim3(64 * kKvStageWaves), 0, st, kp); break;
+        }
+        if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    }
     const ProfileEvents prof = take_profile_events();
     if (prof.before) (void)hipEventRecord(prof.before, st);
     if (launch_prefill<bf16_t, true>(static_cast<int>(device_ordinal), static_cast<int>(head_dim), st, p) != hipSuccess)
