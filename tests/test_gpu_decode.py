@@ -155,6 +155,43 @@ def test_fused_decode_bf16(B, Hq, Hkv, D, rot, lens):
         assert torch.equal(cache.k[b, :, :p].cpu(), case["k"][b, :, :p])
 
 
+def test_fused_decode_many_ragged_sequences():
+    """B > 64: the device-side split plan scans the lengths in several 64-lane
+    passes; ragged lengths including the first token of a sequence."""
+    announce("fused decode B=70 ragged")
+    g = gen(41)
+    lens = torch.randint(0, 300, (70,), generator=g).tolist()
+    lens[5], lens[66] = 0, 299
+    case = make_decode_case(22, 70, 4, 2, 64, 16, lens)
+    out, cache = run_fused(case)
+    ref, k_ref, v_ref, _, _ = oracle_decode(case)
+    check(out, ref, TOL_BF16, "fused B=70")
+    for b in (5, 66):
+        assert torch.equal(cache.v[b, :, lens[b]].cpu(), v_ref[b, :, lens[b]])
+
+
+def test_decode_attend_ragged_with_empty_sequences():
+    """decode_attend over ragged kv_lens with empty sequences (zero output) and
+    B > 64 (multi-pass device plan)."""
+    announce("decode_attend B=67 ragged with empties")
+    g = gen(42)
+    B, Hq, Hkv, D, T = 67, 8, 2, 128, 200
+    lens = torch.randint(0, T + 1, (B,), generator=g)
+    lens[0] = 0
+    lens[66] = 0
+    lens[33] = T
+    q = O.randn_bf16(g, B, Hq, D)
+    k = O.randn_bf16(g, B, Hkv, T, D)
+    v = O.randn_bf16(g, B, Hkv, T, D)
+    out = torch.full((B, Hq * D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    K.decode_attend(0, q.to(DEV), lens.to(torch.int32).to(DEV), K.KvCache(k.to(DEV), v.to(DEV)), out,
+                    q_heads=Hq, kv_heads=Hkv, head_dim=D, max_kv_len=T)
+    torch.cuda.synchronize()
+    ref = O.attention_decode(q.float(), k.float(), v.float(), lens.tolist(), D ** -0.5).reshape(B, Hq * D)
+    check(out, ref, TOL_BF16, "attend B=67")
+    assert torch.all(out[0].float() == 0) and torch.all(out[66].float() == 0)
+
+
 def test_fused_decode_caller_workspace_reuse():
     """A zero-filled caller workspace serves consecutive calls of different
     shapes (the split counters in its first 64 KiB are left at zero)."""
