@@ -741,13 +741,43 @@ struct KvStageParams {
     const uint16_t* sin_t;
     KvView kv;
     uint16_t* vt;           // [Hkv, D, ld]
+    uint16_t* kst;          // fp8 cache: bf16 K rows [Hkv, ld, D] for the attention kernel
     int S, Hkv, off, L, ld, half_rot;
     float eps;
 };
 
 constexpr int kKvStageWaves = 16;  // 4 per SIMD: the rows' memory round trips overlap
 
-template <int D>
+// One row's e4m3 codes with the per-(token, head) absmax scale, as the fused
+// decode append writes them (full_attention_4b.hip:5228-5281, OCP codec): the
+// row's LPR lanes hold 8 values each; returns the lane's 8 codes, sets sc.
+template <int LPR>
+__device__ __forceinline__ u32x2_v quantize_row8(const float (&x)[8], float& sc) {
+    float am = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(x[e]));
+#pragma unroll
+    for (int m = 1; m < LPR; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
+    sc = fmaxf(am / 448.0f, 1e-12f);
+    const float inv = 1.0f / sc;
+    return u32x2_v{f32x4_to_fp8x4(x[0] * inv, x[1] * inv, x[2] * inv, x[3] * inv),
+                   f32x4_to_fp8x4(x[4] * inv, x[5] * inv, x[6] * inv, x[7] * inv)};
+}
+
+// 8 e4m3 codes times their row scale, rounded to bf16.
+__device__ __forceinline__ u32x4_v dequant8_bf16(u32x2_v w, float sc) {
+    u32x4_v r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const f32x2_v lo = fp8x2_to_f32(w[i], false);
+        const f32x2_v hi = fp8x2_to_f32(w[i], true);
+        r[2 * i] = pk2<bf16_t>(lo[0] * sc, lo[1] * sc);
+        r[2 * i + 1] = pk2<bf16_t>(hi[0] * sc, hi[1] * sc);
+    }
+    return r;
+}
+
+template <int D, bool FP8>
 __global__ __launch_bounds__(64 * kKvStageWaves) void kv_stage_kernel(KvStageParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t vtile[64][D + 8];
     constexpr int LPR = D / 8;          // lanes per row
@@ -806,10 +836,35 @@ __global__ __launch_bounds__(64 * kKvStageWaves) void kv_stage_kernel(KvStagePar
                         nq[e] = pk2<bf16_t>(xn[2 * e] * cs[2 * e] + sg * y[2 * e] * sn[2 * e],
                                             xn[2 * e + 1] * cs[2 * e + 1] + sg * y[2 * e + 1] * sn[2 * e + 1]);
                 }
-                st16(reinterpret_cast<uint16_t*>(p.kv.k) + o, nq);
-                st16(reinterpret_cast<uint16_t*>(p.kv.v) + o, vw);
-            } else {
+                if constexpr (!FP8) {
+                    st16(reinterpret_cast<uint16_t*>(p.kv.k) + o, nq);
+                    st16(reinterpret_cast<uint16_t*>(p.kv.v) + o, vw);
+                } else {
+                    // the attention reads this chunk's K and V unquantised (the
+                    // reference runs prefill in bf16 and quantises the cache
+                    // afterwards); the cache gets the e4m3 codes and scales
+                    st16(p.kst + (static_cast<int64_t>(h) * p.ld + pos) * D + 8 * c, nq);
+                    float xk[8], xv[8], sk, sv;
+                    unpack8<bf16_t>(nq, xk);
+                    unpack8<bf16_t>(vw, xv);
+                    const u32x2_v qk8 = quantize_row8<LPR>(xk, sk);
+                    const u32x2_v qv8 = quantize_row8<LPR>(xv, sv);
+                    *reinterpret_cast<u32x2_v*>(p.kv.k + o) = qk8;
+                    *reinterpret_cast<u32x2_v*>(p.kv.v + o) = qv8;
+                    if (c == 0) {
+                        const int64_t so = p.kv.srow(0, h, pos);
+                        p.kv.ks[so] = sk;
+                        p.kv.vs[so] = sv;
+                    }
+                }
+            } else if constexpr (!FP8) {
                 vw = ld16(reinterpret_cast<const uint16_t*>(p.kv.v) + o);
+            } else {
+                // prefix from the fp8 cache: codes times scale, as bf16
+                const int64_t so = p.kv.srow(0, h, pos);
+                st16(p.kst + (static_cast<int64_t>(h) * p.ld + pos) * D + 8 * c,
+                     dequant8_bf16(*reinterpret_cast<const u32x2_v*>(p.kv.k + o), p.kv.ks[so]));
+                vw = dequant8_bf16(*reinterpret_cast<const u32x2_v*>(p.kv.v + o), p.kv.vs[so]);
             }
         }
         st16(&vtile[r][8 * c], vw);
@@ -964,7 +1019,8 @@ extern "C" int supersonic_attn_gfx950_prefill(
     size_t rotary_dim, size_t chunk_len, size_t chunk_start, float eps, float scale, const void* q_proj,
     const void* k_new, const void* v_new, const void* q_norm_w, const void* k_norm_w, const void* cos_table,
     const void* sin_table, const supersonic_kv_cache* cache, void* out) {
-    if (kv_dtype != SUPERSONIC_KV_BF16) return SUPERSONIC_ERR_DTYPE;  // fp8 lane: not yet
+    if (kv_dtype != SUPERSONIC_KV_BF16 && kv_dtype != SUPERSONIC_KV_FP8_E4M3) return SUPERSONIC_ERR_DTYPE;
+    const bool fp8 = kv_dtype == SUPERSONIC_KV_FP8_E4M3;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return SUPERSONIC_ERR_HEAD_DIM;
     if (kv_heads == 0 || q_heads % kv_heads != 0) return SUPERSONIC_ERR_HEADS;
     if (rotary_dim > head_dim || (rotary_dim / 2) % 16 != 0) return SUPERSONIC_ERR_ROTARY;
@@ -972,7 +1028,7 @@ extern "C" int supersonic_attn_gfx950_prefill(
     if (rotary_dim > 0 && (!cos_table || !sin_table)) return SUPERSONIC_ERR_NULL;
     if (chunk_len + chunk_start > 0x7FFFFFFF || q_heads > 4096) return SUPERSONIC_ERR_RANGE;
     KvView kv;
-    if (int rc = make_view(cache, false, &kv)) return rc;
+    if (int rc = make_view(cache, fp8, &kv)) return rc;
     if (kv.bt && kv.page_size % 64 != 0) return SUPERSONIC_ERR_CACHE;
     if (chunk_len == 0) return 0;
     ScopedDevice scoped(static_cast<int>(device_ordinal));
@@ -1006,11 +1062,23 @@ extern "C" int supersonic_attn_gfx950_prefill(
     // position, in one pass
     {
         const int ld = (p.L + 63) / 64 * 64;
-        void* ws = device_workspace(static_cast<int>(device_ordinal),
-                                    static_cast<size_t>(p.Hkv) * head_dim * ld * 2, kWorkspacePrefill);
+        // V^T staging, then (fp8 cache) the bf16 K rows the attention reads
+        const size_t stage_bytes = static_cast<size_t>(p.Hkv) * head_dim * ld * 2;
+        void* ws = device_workspace(static_cast<int>(device_ordinal), fp8 ? 2 * stage_bytes : stage_bytes,
+                                    kWorkspacePrefill);
         if (!ws) return SUPERSONIC_ERR_WORKSPACE;
         p.vt = static_cast<const uint16_t*>(ws);
         p.vt_ld = ld;
+        uint16_t* kst = fp8 ? reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(ws) + stage_bytes) : nullptr;
+        if (fp8) {
+            // the attention kernel's K: the contiguous staging rows
+            KvView ks{};
+            ks.k = reinterpret_cast<uint8_t*>(kst);
+            ks.head_stride = static_cast<int64_t>(ld) * head_dim;
+            ks.seq_stride = static_cast<int64_t>(p.Hkv) * ld * head_dim;
+            ks.page_size = 1;
+            p.kv = ks;
+        }
         KvStageParams kp{};
         kp.k_new = static_cast<const uint16_t*>(k_new);
         kp.v_new = static_cast<const uint16_t*>(v_new);
@@ -1019,6 +1087,7 @@ extern "C" int supersonic_attn_gfx950_prefill(
         kp.sin_t = static_cast<const uint16_t*>(sin_table);
         kp.kv = kv;
         kp.vt = static_cast<uint16_t*>(ws);
+        kp.kst = kst;
         kp.S = static_cast<int>(chunk_len);
         kp.Hkv = static_cast<int>(kv_heads);
         kp.off = static_cast<int>(chunk_start);
@@ -1027,10 +1096,14 @@ extern "C" int supersonic_attn_gfx950_prefill(
         kp.half_rot = static_cast<int>(rotary_dim / 2);
         kp.eps = eps;
         const dim3 grid(ld / 64, kp.Hkv);
-        switch (head_dim) {
-        case 64: hipLaunchKernelGGL(kv_stage_kernel<64>, grid, dim3(64 * kKvStageWaves), 0, st, kp); break;
-        case 128: hipLaunchKernelGGL(kv_stage_kernel<128>, grid, dim3(64 * kKvStageWaves), 0, st, kp); break;
-        default: hipLaunchKernelGGL(kv_stage_kernel<256>, grid, dim3(64 * kKvStageWaves), 0, st, kp); break;
+        const dim3 blk(64 * kKvStageWaves);
+        switch (head_dim * 2 + (fp8 ? 1 : 0)) {
+        case 128: hipLaunchKernelGGL((kv_stage_kernel<64, false>), grid, blk, 0, st, kp); break;
+        case 129: hipLaunchKernelGGL((kv_stage_kernel<64, true>), grid, blk, 0, st, kp); break;
+        case 256: hipLaunchKernelGGL((kv_stage_kernel<128, false>), grid, blk, 0, st, kp); break;
+        case 257: hipLaunchKernelGGL((kv_stage_kernel<128, true>), grid, blk, 0, st, kp); break;
+        case 512: hipLaunchKernelGGL((kv_stage_kernel<256, false>), grid, blk, 0, st, kp); break;
+        default: hipLaunchKernelGGL((kv_stage_kernel<256, true>), grid, blk, 0, st, kp); break;
         }
         if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
     }

@@ -5,7 +5,8 @@ import os
 import pytest
 import torch
 
-from gpu_util import DEV, TOL_BF16, announce, check, gen
+from gpu_util import DEV, TOL_BF16, announce, check, fp8_rows, gen
+from oracle import fp8_codec
 from oracle import attn_oracle as O
 from supersonic_amd import kernel_ffi as K
 
@@ -151,3 +152,42 @@ def test_fused_prefill_config3_full_size():
     ref, _, _ = O.prefill_layer(c["shape"], c["q_proj"], c["k_new"], c["v_new"], c["qw"], c["kw"], c["cos"],
                                 c["sin"], 0)
     check(out, ref, TOL_BF16, "config3")
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,D,rot,start", [(200, 8, 2, 128, 32, 130), (64, 4, 1, 256, 64, 0)])
+def test_fused_prefill_fp8_cache(S, Hq, Hkv, D, rot, start):
+    """FP8 (OCP e4m3) cache: the prefix is read back dequantised, the chunk's own
+    K/V enter the attention unquantised (the reference runs prefill in bf16 and
+    quantises the cache afterwards), and the appended codes and scales are the
+    oracle quantiser's, bit for bit."""
+    announce(f"fused prefill fp8 S={S} Hq={Hq} Hkv={Hkv} D={D} start={start}")
+    c = fused_case(74, S, Hq, Hkv, D, rot, start)
+    cap = start + S + 7
+    kq = torch.zeros(1, Hkv, cap, D, dtype=torch.uint8)
+    vq = torch.zeros_like(kq)
+    ks = torch.zeros(1, Hkv, cap, dtype=torch.float32)
+    vs = torch.zeros_like(ks)
+    pk, pks = fp8_rows(c["prefix_k"])
+    pv, pvs = fp8_rows(c["prefix_v"])
+    kq[0, :, :start], ks[0, :, :start] = pk, pks
+    vq[0, :, :start], vs[0, :, :start] = pv, pvs
+    cache = K.KvCache(kq.to(DEV), vq.to(DEV), ks.to(DEV), vs.to(DEV))
+    out = run_fused_prefill(c, start, cache)
+    # prefix as the kernel reads it: codes times scale, rounded to bf16
+    deq = lambda q, sc: (torch.from_numpy(fp8_codec.decode(q.numpy())) * sc[..., None]).bfloat16().float()
+    ref, kch, vch = O.prefill_layer(c["shape"], c["q_proj"], c["k_new"], c["v_new"], c["qw"], c["kw"], c["cos"],
+                                    c["sin"], start, deq(pk, pks), deq(pv, pvs))
+    check(out, ref, TOL_BF16, "fused prefill fp8")
+    # V reaches the cache unchanged, so its codes and scales are the quantiser's bit for bit
+    ev, evs = fp8_rows(vch)
+    assert torch.equal(cache.v[0, :, start:start + S].cpu(), ev)
+    assert torch.equal(cache.v_scale[0, :, start:start + S].cpu(), evs)
+    # K passes through norm and RoPE, whose bf16 results may differ from the oracle's by
+    # one ulp: scales agree to that ulp, and the dequantised rows to one e4m3 step
+    ek, eks = fp8_rows(kch)
+    gk, gks = cache.k[0, :, start:start + S].cpu(), cache.k_scale[0, :, start:start + S].cpu()
+    assert torch.allclose(gks, eks, rtol=2 ** -7, atol=0)
+    assert (gk == ek).float().mean().item() > 0.98
+    kd = deq(gk, gks) - kch
+    assert kd.abs().max().item() <= 2 ** -3 * kch.abs().amax(-1).max().item()
+    assert torch.equal(cache.k[0, :, :start].cpu(), pk)  # the prefix is untouched
