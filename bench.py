@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
-    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|copy")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|oproj|copy")
     return ap.parse_args()
 
 
@@ -104,7 +104,8 @@ def main():
     if not args.skip_cpu:
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
-        out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "fp8", "mixed")}
+        out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "fp8", "mixed",
+                                                          "oproj")}
     print(json.dumps(out))
 
 
@@ -312,6 +313,31 @@ class Workloads:
                 "decode_gbs": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9,
                 "decode_frac": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 "lens_sum": sum(lens)}
+
+    def oproj(self):
+        """Output projection + residual after the attention, config-2 decode step:
+        8 rows, attn 16x256 = 4096 -> hidden 4096 (Qwen3.5-9B hidden size), bf16
+        weights.  16 weight copies (512 MB) rotate so no step finds W in the
+        256 MB last-level cache, as across a model's layers."""
+        torch, K = self.torch, self.K
+        rows, hid, adim, copies = 8, 4096, 4096, 16
+        ws = [self.randn(hid, adim, seed=20 + c) * (adim ** -0.5) for c in range(copies)]
+        ws = [w.to(torch.bfloat16).contiguous() for w in ws]
+        attn = self.randn(rows, adim, seed=40)
+        hidden = self.randn(rows, hid, seed=41)
+
+        def step(i):
+            K.o_proj_residual(0, attn, ws[i], hidden)
+        step_ms, kern_ms, _ = self.timed(step, copies)
+        kern_bytes = hid * adim * 2 + rows * adim * 2 + rows * hid * 4
+        ach = kern_bytes / (kern_ms * 1e-3) / 1e9
+        del ws
+        torch.cuda.empty_cache()
+        return {"workload": "o_proj + residual, 8 rows, 4096 -> 4096, bf16", "ms_per_step": step_ms,
+                "kernel_ms": kern_ms, "bytes": kern_bytes,
+                "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "skinny_kernel",
+                             "bytes_per_launch": kern_bytes}}
 
     def copy(self):
         """Plain device copy of known size, to calibrate FETCH_SIZE/WRITE_SIZE counters."""

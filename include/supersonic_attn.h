@@ -136,6 +136,24 @@ int supersonic_qwen35_hip_split_qgate(
     int dtype, size_t device_ordinal, size_t s, size_t num_heads, size_t head_dim,
     const void* src, void* query_out, void* gate_out);
 
+/* out[b] = bf16(lhs[b] . rhs[b]^T) with fp32 accumulation: lhs [batch, m, k],
+ * rhs [batch, n, k], out [batch, m, n], bf16 only (the projections, o_proj
+ * included, of prefill_engine.rs:356-414).  Replaces
+ * kernels/full_attention_bridge_4b.cpp:3683-3704 (kernel full_attention_4b.hip:2513-2575),
+ * bound at prefill_ffi.rs:782-792.  m <= 64: HBM-streaming MFMA kernel; larger m:
+ * hipBLASLt.  Status: 272 bad dtype, 270 launch, 271 sync. */
+int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(
+    int dtype, size_t device_ordinal, size_t batch_elems, int m, int n, int k,
+    const void* lhs, const void* rhs, void* out);
+
+/* out = lhs + rhs elementwise (fp32 add, one rounding): the residual add of
+ * prefill_engine.rs:419-429.  Replaces kernels/prefill_helpers_bridge.cpp:281-290
+ * (kernel prefill_helpers.hip:59-68), bound at prefill_ffi.rs:661-668.
+ * dtype 0/1/2.  Status: 300 bad dtype, 301 launch, 302 sync. */
+int supersonic_qwen35_hip_element_add(
+    int dtype, size_t device_ordinal, size_t total_elems, const void* lhs, const void* rhs,
+    void* out);
+
 /* ------------------------------------------------------------------------- */
 /* 2. Native fused entry points (no reference counterpart; they replace the  */
 /*    a1-a9 chain of prefill_engine.rs:1951-2308 and the megakernel's        */
@@ -213,6 +231,20 @@ int supersonic_attn_gfx950_prefill(
     const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
     const supersonic_kv_cache* cache, void* out);
 
+/* Output projection with the residual add, after the gated attention:
+ *   hidden[r, j] = bf16(hidden[r, j] + bf16(sum_c attn[r, c] * o_proj_w[j, c]))
+ * attn [rows, attn_dim] bf16 (the fused decode/prefill `out`), o_proj_w
+ * [hidden_dim, attn_dim] bf16, hidden [rows, hidden_dim] updated in place, bf16
+ * (hidden_dtype 2, the prefill engine's hidden) or f32 holding bf16 values
+ * (hidden_dtype 1, the megakernel's hidden_f32).  Replaces the megakernel's
+ * step G (full_attention_4b.hip:5481-5577) and matmul_proj + residual_add of
+ * prefill_engine.rs:2308-2334.  rows <= 64 with attn_dim % 8 == 0: one
+ * HBM-streaming MFMA kernel with the residual fused; otherwise hipBLASLt and a
+ * residual kernel.  Asynchronous on `stream`. */
+int supersonic_attn_gfx950_o_proj_residual(
+    size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim,
+    size_t attn_dim, const void* attn, const void* o_proj_w, void* hidden);
+
 /* OCP e4m3 variant of supersonic_qwen35_4b_hip_quantize_kv_to_fp8: same
  * layout and scale rule (scale = max(absmax/448, 1e-12)), hardware OCP
  * round-to-nearest-even codes, the codec the fused entry points write.
@@ -223,7 +255,7 @@ int supersonic_attn_gfx950_quantize_kv_fp8_ocp(
 
 /* Benchmark hook (no reference counterpart): two hipEvent_t recorded on the
  * launch stream right before and right after the dominant kernel (split-K
- * decode kernel, MFMA prefill kernel) of the next fused-entry call on any
+ * decode kernel, MFMA prefill kernel, o_proj kernel) of the next fused-entry call on any
  * thread; the pair is consumed by that call.  NULL, NULL clears it. */
 void supersonic_attn_gfx950_set_profile_events(void* before, void* after);
 

@@ -283,6 +283,33 @@ def decode_layer(shape: LayerShape, q_proj, k_raw, v_raw, q_norm_w, k_norm_w, co
 # ---------------------------------------------------------------------------
 # Seeded synthetic inputs (same generator on CPU for oracle and GPU runs)
 # ---------------------------------------------------------------------------
+# ---------------------------------------------------------------------------
+# f1: output projection and residual add
+# ---------------------------------------------------------------------------
+def matmul_rhs_transposed(lhs: torch.Tensor, rhs: torch.Tensor) -> torch.Tensor:
+    """``out[b, m, n] = bf16(sum_k lhs[b, m, k] * rhs[b, n, k])``, fp32 accumulation:
+    ``supersonic_qwen35_matmul_rhs_transposed_tiled_kernel`` (full_attention_4b.hip:2513-2575,
+    bridge full_attention_bridge_4b.cpp:3584-3611).  That kernel gives rhs its own
+    batch dimension (``rhs_base = batch * n * k``); the host fallback
+    (metal_host.rs:213-245) shares one ``[n, k]`` rhs.  Both agree at batch 1."""
+    return bf16r(torch.matmul(lhs.to(F32), rhs.to(F32).transpose(-1, -2)))
+
+
+def element_add(lhs: torch.Tensor, rhs: torch.Tensor) -> torch.Tensor:
+    """``pfx_element_add_kernel`` (prefill_helpers.hip:59-68): fp32 add, one rounding
+    to the element type (here bf16)."""
+    return bf16r(lhs.to(F32) + rhs.to(F32))
+
+
+def o_proj_residual(attn: torch.Tensor, w: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
+    """Output projection plus residual, two roundings: ``add = bf16(attn . w_j)`` then
+    ``hidden = bf16(hidden + add)``.  Decode: megakernel step G
+    (full_attention_4b.hip:5481-5577, bf16 weights :5551-5568, the two
+    ``bf16_round_rne_f32_finite`` at :5572-5574).  Prefill: ``matmul_proj`` to a bf16
+    buffer, then ``residual_add`` (prefill_engine.rs:2308-2334, 419-429)."""
+    return element_add(hidden, matmul_rhs_transposed(attn, w))
+
+
 def randn_bf16(gen: torch.Generator, *shape, std: float = 1.0, mean: float = 0.0) -> torch.Tensor:
     return (torch.randn(*shape, generator=gen, dtype=F32) * std + mean).to(BF16)
 

@@ -146,6 +146,15 @@ __device__ __forceinline__ void st16(void* p, const u32x4_v& v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Device-coherent (sc1) relaxed accesses: visible across the XCDs' L2s without
+// a device-wide fence.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace ssa
 
 // ----------------------------------------------------------------------------
@@ -176,7 +185,10 @@ struct ScopedDevice {
 // prefill V^T staging never share memory.
 constexpr int kWorkspaceDecode = 0;
 constexpr int kWorkspacePrefill = 1;
-constexpr int kWorkspaceSlots = 2;
+constexpr int kWorkspaceProj = 2;    // GEMM output of the large-row o_proj path
+constexpr int kWorkspaceProjLt = 3;  // hipBLASLt workspace
+constexpr int kWorkspaceSkinny = 4;  // split-k partials and arrival counters of the o_proj kernel
+constexpr int kWorkspaceSlots = 5;
 void* device_workspace(int device, size_t bytes, int slot);
 
 // Compute units of `device` (cached; 256 on MI355X), 0 if the query fails.

@@ -132,15 +132,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const uint8_t* ba
     return __builtin_amdgcn_make_buffer_rsrc(u, static_cast<short>(0), bytes, 0x00020000);
 }
 
-// Device-coherent (sc1) relaxed accesses: visible across the XCDs' L2s without
-// a device-wide fence.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <typename QT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);

@@ -1,0 +1,419 @@
+// Output projection after the gated attention, with the residual add.
+//
+//   decode:  hidden[r] = bf16(hidden[r] + bf16(attn[r] . W_o^T))
+//            (megakernel step G, kernels/full_attention_4b.hip:5481-5577, bf16
+//            weight branch :5551-5574)
+//   prefill: out = bf16(lhs . rhs^T) then hidden = bf16(hidden + out)
+//            (matmul_proj + residual_add, crates/runner/src/prefill_engine.rs:2308-2334,
+//            kernels full_attention_4b.hip:2513-2575 and prefill_helpers.hip:59-68)
+//
+// Few rows (decode batches, <= 12 by default) make a weight stream: W [n, k]
+// bf16 is read once from HBM and the kernel is HBM-bound.  A workgroup owns 16
+// output columns (16 rows of W); its 8 waves split k and load W straight into
+// the B-operand layout of v_mfma_f32_16x16x32_bf16 (lane l: W row n0 + l%16, 8
+// consecutive k at 8*(l/16)), with the activation rows as the A operand (16
+// rows per MFMA, zero past m).  8 k-steps (8 x 16 B per lane) are in flight per
+// load batch, which keeps a wave under 128 VGPRs so two workgroups share a CU.
+// The waves' partial sums meet in LDS; the epilogue rounds to bf16 and adds the
+// residual with the reference's second rounding.  When there are fewer column
+// blocks than CUs, k is also split over workgroups: each stores its fp32 partial
+// block with device-coherent stores and the last to arrive adds the slices in
+// slice order (deterministic) and runs the epilogue.
+//
+// More rows are plain GEMMs and go to hipBLASLt (bf16 in/out, fp32
+// accumulate), followed by the residual kernel where one is asked for.
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "common.hpp"
+#include "supersonic_attn.h"
+
+namespace ssa {
+
+struct SkinnyParams {
+    const uint16_t* x;    // [batch][m][k] bf16
+    const uint16_t* w;    // [batch][n][k] bf16
+    void* out;            // [batch][m][n] (OT)
+    const void* res;      // residual [batch][m][n] (OT), may alias out
+    float* part;          // split k: [batch * column blocks][ks_count][MB*16*64] partial sums
+    unsigned* arrivals;   // split k: [batch * column blocks] counters, zero between calls
+    int m, n, k;
+    int ks_count, slice;  // k split over ks_count workgroups of `slice` 32-wide k-steps
+    int64_t x_bs, w_bs, o_bs;  // batch strides in elements
+};
+
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyCB = 1;                        // 16-column blocks per workgroup
+constexpr int kSkinnyKP = kSkinnyWaves / kSkinnyCB;  // k parts per workgroup (one per wave group)
+constexpr int kSkinnySteps = 8;                     // 32-wide k-steps per load batch (<= 128 VGPRs)
+constexpr int kSkinnyCols = 16 * kSkinnyCB;         // W rows (output columns) per workgroup
+constexpr int kSkinnyMaxM = 64;                     // hard limit (4 row blocks)
+constexpr int kSkinnyDefaultM = 12;                 // measured crossover with hipBLASLt
+constexpr size_t kSkinnyArrivalBytes = 64 << 10;  // counters at a fixed offset, ahead of the partials
+
+__device__ __forceinline__ bf16x8_v as_bf16x8(const u32x4_v& v) { return __builtin_bit_cast(bf16x8_v, v); }
+
+template <typename OT, bool RES>
+__device__ __forceinline__ void skinny_store(const SkinnyParams& p, int b, int row, int col, float s) {
+    if (row >= p.m || col >= p.n) return;
+    float y = bf16_round(s);
+    const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * p.n + col;
+    if constexpr (RES) y = bf16_round(load_f32<OT>(static_cast<const OT*>(p.res), o) + y);
+    store_f32<OT>(static_cast<OT*>(p.out), o, y);
+}
+
+// Workgroup (column block cb, k slice ks, batch b): 64 W rows x `slice` k-steps.
+// Wave w: columns cb*64 + 16*(w&3) .. +16, half (w>>2) of the slice.  The four
+// waves of a half read the same activation addresses, so the activations cross
+// L2 once per workgroup; splitting k over workgroups keeps that at
+// m*k*2*(column blocks) bytes in all, not per 16 columns.
+template <typename OT, bool RES, int MB>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_kernel(SkinnyParams p) {
+    __shared__ float red[kSkinnyKP][kSkinnyCB][MB][256];
+    __shared__ int last_s;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int cbw = wave % kSkinnyCB, kh = wave / kSkinnyCB;
+    const int cb = blockIdx.x, ks = blockIdx.y, b = blockIdx.z;
+    const uint16_t* x = p.x + b * p.x_bs;
+    const uint16_t* w = p.w + b * p.w_bs;
+    const int T = (p.k + 31) / 32;
+    const int sb0 = ks * p.slice;
+    const int sb1 = min(sb0 + p.slice, T);
+    const int half = (max(sb1 - sb0, 0) + kSkinnyKP - 1) / kSkinnyKP;
+    const int s0 = sb0 + kh * half;
+    const int s1 = min(s0 + half, sb1);
+    const int col = lane & 15;
+    const int kq = (lane >> 4) * 8;
+    const int n_w = cb * kSkinnyCols + cbw * 16 + col;
+    const bool nvalid = n_w < p.n;
+    const uint16_t* wrow = w + static_cast<int64_t>(min(n_w, p.n - 1)) * p.k + kq;
+    const uint16_t* xrow[MB];
+    bool mvalid[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int r = mb * 16 + col;
+        mvalid[mb] = r < p.m;
+        xrow[mb] = x + static_cast<int64_t>(min(r, p.m - 1)) * p.k + kq;
+    }
+    f32x4_v acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+    const u32x4_v zero = {0u, 0u, 0u, 0u};
+    for (int sb = s0; sb < s1; sb += kSkinnySteps) {
+        u32x4_v wv[kSkinnySteps];
+#pragma unroll
+        for (int j = 0; j < kSkinnySteps; ++j) {
+            const int s = sb + j;
+            wv[j] = (s < s1 && nvalid && s * 32 + kq < p.k) ? ld16(wrow + s * 32) : zero;
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            u32x4_v xv[kSkinnySteps];
+#pragma unroll
+            for (int j = 0; j < kSkinnySteps; ++j) {
+                const int s = sb + j;
+                xv[j] = (s < s1 && mvalid[mb] && s * 32 + kq < p.k) ? ld16(xrow[mb] + s * 32) : zero;
+            }
+#pragma unroll
+            for (int j = 0; j < kSkinnySteps; ++j)
+                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[j]), as_bf16x8(wv[j]), acc[mb], 0, 0, 0);
+        }
+    }
+    // accumulator layout: lane l, element i -> row 4*(l/16)+i, column l%16
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[kh][cbw][mb][(4 * (lane >> 4) + i) * 16 + col] = acc[mb][i];
+    __syncthreads();
+    // element e of the workgroup's block: column block c = e / (MB*256), row block, 16x16 entry
+    constexpr int NE = kSkinnyCB * MB * 256;
+    const bool split = p.ks_count > 1;
+    const int64_t blk = static_cast<int64_t>(b) * gridDim.x + cb;
+    for (int e = tid; e < NE; e += 64 * kSkinnyWaves) {
+        const int c = e / (MB * 256), mb = (e / 256) % MB, r = e & 255;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < kSkinnyKP; ++q) sum += red[q][c][mb][r];
+        if (split)
+            store_agent(p.part + (blk * p.ks_count + ks) * NE + e, sum);
+        else
+            skinny_store<OT, RES>(p, b, mb * 16 + (r >> 4), cb * kSkinnyCols + c * 16 + (r & 15), sum);
+    }
+    if (!split) return;
+    // The last workgroup of the column block to arrive adds the k slices in
+    // slice order (the result does not depend on arrival order) and stores.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
+    __syncthreads();
+    if (tid == 0) last_s = atomicAdd(&p.arrivals[blk], 1u) == static_cast<unsigned>(p.ks_count - 1);
+    __syncthreads();
+    if (!last_s) return;
+    const float* base = p.part + blk * p.ks_count * NE;
+    for (int e = tid; e < NE; e += 64 * kSkinnyWaves) {
+        const int c = e / (MB * 256), mb = (e / 256) % MB, r = e & 255;
+        float sum = 0.f;
+        for (int q = 0; q < p.ks_count; ++q) sum += load_agent(base + q * NE + e);
+        skinny_store<OT, RES>(p, b, mb * 16 + (r >> 4), cb * kSkinnyCols + c * 16 + (r & 15), sum);
+    }
+    if (tid == 0) p.arrivals[blk] = 0u;  // every slice has arrived: ready for the next call
+}
+
+// hidden = bf16(hidden + y) over `total` elements (y bf16).
+template <typename OT>
+__global__ void residual_add_kernel(size_t total, const uint16_t* y, OT* hidden) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        store_f32<OT>(hidden, i, bf16_round(load_f32<OT>(hidden, i) + bf16_bits_to_f32(y[i])));
+}
+
+// out = T(float(lhs) + float(rhs)): pfx_element_add_kernel (prefill_helpers.hip:59-68).
+template <typename T>
+__global__ void element_add_kernel(size_t total, const T* lhs, const T* rhs, T* out) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        store_f32<T>(out, i, load_f32<T>(lhs, i) + load_f32<T>(rhs, i));
+}
+
+inline unsigned stride_blocks(size_t n) {
+    const size_t b = (n + 255) / 256;
+    return static_cast<unsigned>(b < 8192 ? (b ? b : 1) : 8192);
+}
+
+// Largest row count the streaming kernel takes (SUPERSONIC_PROJ_SKINNY_MAX_M,
+// default 12, at most 64, read per call); more rows go to hipBLASLt.
+int skinny_max_m() {
+    const char* e = getenv("SUPERSONIC_PROJ_SKINNY_MAX_M");
+    const int x = e ? atoi(e) : kSkinnyDefaultM;
+    return x < 0 ? 0 : (x > kSkinnyMaxM ? kSkinnyMaxM : x);
+}
+
+bool skinny_fits(int m, int k, const void* x, const void* w) {
+    return m >= 1 && m <= skinny_max_m() && k % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+}
+
+// Plans the k split (enough workgroups to cover the CUs, at least 8 k-steps
+// per wave) and launches.  Returns a SUPERSONIC status (0 = ok).
+template <typename OT, bool RES>
+int launch_skinny(int dev, hipStream_t st, int batch, SkinnyParams p) {
+    const int ncb = (p.n + kSkinnyCols - 1) / kSkinnyCols;
+    const int T = (p.k + 31) / 32;
+    const int MB = (p.m + 15) / 16;
+    const int64_t wgs = static_cast<int64_t>(ncb) * batch;
+    const int cus = device_cu_count(dev) > 0 ? device_cu_count(dev) : 256;
+    int ks = 1;
+    while (wgs * ks * 2 <= cus && T / (ks * 2) >= kSkinnyKP * 8) ks *= 2;
+    if (wgs > static_cast<int64_t>(kSkinnyArrivalBytes / 4)) ks = 1;
+    p.ks_count = ks;
+    p.slice = (T + ks - 1) / ks;
+    if (ks > 1) {
+        const size_t part_bytes = static_cast<size_t>(wgs) * ks * kSkinnyCB * MB * 256 * sizeof(float);
+        uint8_t* ws = static_cast<uint8_t*>(device_workspace(dev, kSkinnyArrivalBytes + part_bytes, kWorkspaceSkinny));
+        if (!ws) return SUPERSONIC_ERR_WORKSPACE;
+        p.arrivals = reinterpret_cast<unsigned*>(ws);
+        p.part = reinterpret_cast<float*>(ws + kSkinnyArrivalBytes);
+    }
+    const dim3 grid(ncb, ks, batch), blk(64 * kSkinnyWaves);
+    switch (MB) {
+    case 1: hipLaunchKernelGGL((skinny_kernel<OT, RES, 1>), grid, blk, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((skinny_kernel<OT, RES, 2>), grid, blk, 0, st, p); break;
+    case 3: hipLaunchKernelGGL((skinny_kernel<OT, RES, 3>), grid, blk, 0, st, p); break;
+    default: hipLaunchKernelGGL((skinny_kernel<OT, RES, 4>), grid, blk, 0, st, p); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
+}
+
+// ---------------------------------------------------------------------------
+// hipBLASLt for the GEMM-sized calls: out[b] (m x n, row-major) = lhs[b] . rhs[b]^T.
+// In hipBLASLt's column-major terms that is D (n x m, ld n) = op_T(A: k x n, ld k) . B (k x m, ld k).
+// ---------------------------------------------------------------------------
+namespace {
+struct LtPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+struct LtDevice {
+    hipblasLtHandle_t handle = nullptr;
+    std::map<std::tuple<int, int, int, int>, LtPlan> plans;
+};
+std::mutex g_lt_mutex;
+std::map<int, LtDevice> g_lt;
+constexpr size_t kLtWorkspace = 32u << 20;
+
+bool make_layout(hipblasLtMatrixLayout_t* l, uint64_t rows, uint64_t cols, int64_t ld, int batch, int64_t stride) {
+    if (hipblasLtMatrixLayoutCreate(l, HIP_R_16BF, rows, cols, ld) != HIPBLAS_STATUS_SUCCESS) return false;
+    if (batch > 1) {
+        const int32_t bc = batch;
+        if (hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
+                HIPBLAS_STATUS_SUCCESS ||
+            hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &stride,
+                                              sizeof(stride)) != HIPBLAS_STATUS_SUCCESS)
+            return false;
+    }
+    return true;
+}
+}  // namespace
+
+// 0 on success, 1 when hipBLASLt has no plan for the shape, 2 on a launch error.
+int lt_gemm(int dev, hipStream_t st, int batch, int m, int n, int k, const void* lhs, const void* rhs, void* out) {
+    std::lock_guard<std::mutex> lock(g_lt_mutex);
+    LtDevice& D = g_lt[dev];
+    if (!D.handle && hipblasLtCreate(&D.handle) != HIPBLAS_STATUS_SUCCESS) {
+        D.handle = nullptr;
+        return 1;
+    }
+    void* ws = device_workspace(dev, kLtWorkspace, kWorkspaceProjLt);
+    if (!ws) return 2;
+    const auto key = std::make_tuple(batch, m, n, k);
+    auto it = D.plans.find(key);
+    if (it == D.plans.end()) {
+        LtPlan P;
+        const hipblasOperation_t opA = HIPBLAS_OP_T, opB = HIPBLAS_OP_N;
+        if (hipblasLtMatmulDescCreate(&P.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+            hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opA, sizeof(opA)) !=
+                HIPBLAS_STATUS_SUCCESS ||
+            hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opB, sizeof(opB)) !=
+                HIPBLAS_STATUS_SUCCESS ||
+            !make_layout(&P.a, k, n, k, batch, static_cast<int64_t>(n) * k) ||
+            !make_layout(&P.b, k, m, k, batch, static_cast<int64_t>(m) * k) ||
+            !make_layout(&P.d, n, m, n, batch, static_cast<int64_t>(m) * n))
+            return 1;
+        hipblasLtMatmulPreference_t pref;
+        if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return 1;
+        const uint64_t wsb = kLtWorkspace;
+        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
+        hipblasLtMatmulHeuristicResult_t res[1];
+        int found = 0;
+        const hipblasStatus_t hs =
+            hipblasLtMatmulAlgoGetHeuristic(D.handle, P.desc, P.a, P.b, P.d, P.d, pref, 1, res, &found);
+        hipblasLtMatmulPreferenceDestroy(pref);
+        if (hs != HIPBLAS_STATUS_SUCCESS || found < 1) return 1;
+        P.algo = res[0].algo;
+        it = D.plans.emplace(key, P).first;
+    }
+    const LtPlan& P = it->second;
+    const float alpha = 1.f, beta = 0.f;
+    if (hipblasLtMatmul(D.handle, P.desc, &alpha, rhs, P.a, lhs, P.b, &beta, out, P.d, out, P.d, &P.algo, ws,
+                        kLtWorkspace, st) != HIPBLAS_STATUS_SUCCESS)
+        return 2;
+    return 0;
+}
+
+}  // namespace ssa
+
+using namespace ssa;
+
+// Drop-in for kernels/full_attention_bridge_4b.cpp:3683-3704 (kernel
+// full_attention_4b.hip:2513-2575), bound at crates/kernel-ffi/src/prefill_ffi.rs:782-792.
+extern "C" int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(int dtype, size_t device_ordinal,
+                                                                    size_t batch_elems, int m, int n, int k,
+                                                                    const void* lhs, const void* rhs, void* out) {
+    if (dtype != SUPERSONIC_DTYPE_BF16) return 272;
+    const int dev = static_cast<int>(device_ordinal);
+    ScopedDevice scoped(dev);
+    if (batch_elems > 0 && m > 0 && n > 0) {
+        const int batch = static_cast<int>(batch_elems);
+        if (k <= 0 || skinny_fits(m, k, lhs, rhs)) {
+            SkinnyParams p{};
+            p.x = static_cast<const uint16_t*>(lhs);
+            p.w = static_cast<const uint16_t*>(rhs);
+            p.out = out;
+            p.m = m;
+            p.n = n;
+            p.k = k > 0 ? k : 0;
+            p.x_bs = static_cast<int64_t>(m) * p.k;
+            p.w_bs = static_cast<int64_t>(n) * p.k;
+            p.o_bs = static_cast<int64_t>(m) * n;
+            if (m > skinny_max_m()) {  // k == 0 with many rows: the product is zero
+                if (hipMemsetAsync(out, 0, batch_elems * m * n * 2, nullptr) != hipSuccess) return 270;
+            } else if (const int rc = launch_skinny<bf16_t, false>(dev, nullptr, batch, p)) {
+                return rc == SUPERSONIC_ERR_WORKSPACE ? 2 : 270;
+            }
+        } else if (lt_gemm(dev, nullptr, batch, m, n, k, lhs, rhs, out) != 0) {
+            return 270;
+        }
+    }
+    if (hipDeviceSynchronize() != hipSuccess) return 271;
+    return 0;
+}
+
+// Drop-in for kernels/prefill_helpers_bridge.cpp:281-290, bound at prefill_ffi.rs:661-668.
+extern "C" int supersonic_qwen35_hip_element_add(int dtype, size_t device_ordinal, size_t total_elems,
+                                                 const void* lhs, const void* rhs, void* out) {
+    if (dtype < 0 || dtype > 2) return 300;
+    ScopedDevice scoped(static_cast<int>(device_ordinal));
+    if (total_elems) {
+        const dim3 grid(stride_blocks(total_elems)), blk(256);
+        switch (dtype) {
+        case 0:
+            hipLaunchKernelGGL((element_add_kernel<f16_t>), grid, blk, 0, nullptr, total_elems,
+                               static_cast<const f16_t*>(lhs), static_cast<const f16_t*>(rhs), static_cast<f16_t*>(out));
+            break;
+        case 1:
+            hipLaunchKernelGGL((element_add_kernel<float>), grid, blk, 0, nullptr, total_elems,
+                               static_cast<const float*>(lhs), static_cast<const float*>(rhs), static_cast<float*>(out));
+            break;
+        default:
+            hipLaunchKernelGGL((element_add_kernel<bf16_t>), grid, blk, 0, nullptr, total_elems,
+                               static_cast<const bf16_t*>(lhs), static_cast<const bf16_t*>(rhs),
+                               static_cast<bf16_t*>(out));
+            break;
+        }
+        if (hipGetLastError() != hipSuccess) return 301;
+    }
+    if (hipDeviceSynchronize() != hipSuccess) return 302;
+    return 0;
+}
+
+extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, void* stream, int hidden_dtype,
+                                                      size_t rows, size_t hidden_dim, size_t attn_dim,
+                                                      const void* attn, const void* o_proj_w, void* hidden) {
+    if (hidden_dtype != SUPERSONIC_DTYPE_BF16 && hidden_dtype != SUPERSONIC_DTYPE_F32) return SUPERSONIC_ERR_DTYPE;
+    if (rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || attn_dim > 0x7FFFFFFF) return SUPERSONIC_ERR_RANGE;
+    if (rows == 0 || hidden_dim == 0) return 0;
+    if (!hidden || (attn_dim && (!attn || !o_proj_w))) return SUPERSONIC_ERR_NULL;
+    const int dev = static_cast<int>(device_ordinal);
+    ScopedDevice scoped(dev);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int m = static_cast<int>(rows), n = static_cast<int>(hidden_dim), k = static_cast<int>(attn_dim);
+    const bool f32 = hidden_dtype == SUPERSONIC_DTYPE_F32;
+    const ProfileEvents ev = take_profile_events();
+    if (ev.before) (void)hipEventRecord(ev.before, st);
+    if (skinny_fits(m, k, attn, o_proj_w)) {
+        SkinnyParams p{};
+        p.x = static_cast<const uint16_t*>(attn);
+        p.w = static_cast<const uint16_t*>(o_proj_w);
+        p.out = hidden;
+        p.res = hidden;
+        p.m = m;
+        p.n = n;
+        p.k = k;
+        const int rc = f32 ? launch_skinny<float, true>(dev, st, 1, p) : launch_skinny<bf16_t, true>(dev, st, 1, p);
+        if (rc) return rc;
+    } else {
+        const size_t total = rows * hidden_dim;
+        void* y = device_workspace(dev, total * 2, kWorkspaceProj);
+        if (!y) return SUPERSONIC_ERR_WORKSPACE;
+        if (k == 0) {
+            if (hipMemsetAsync(y, 0, total * 2, st) != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+        } else if (lt_gemm(dev, st, 1, m, n, k, attn, o_proj_w, y) != 0) {
+            return SUPERSONIC_ERR_LAUNCH;
+        }
+        const dim3 grid(stride_blocks(total)), blk(256);
+        if (f32)
+            hipLaunchKernelGGL((residual_add_kernel<float>), grid, blk, 0, st, total, static_cast<const uint16_t*>(y),
+                               static_cast<float*>(hidden));
+        else
+            hipLaunchKernelGGL((residual_add_kernel<bf16_t>), grid, blk, 0, st, total,
+                               static_cast<const uint16_t*>(y), static_cast<bf16_t*>(hidden));
+        if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    }
+    if (ev.after) (void)hipEventRecord(ev.after, st);
+    return 0;
+}

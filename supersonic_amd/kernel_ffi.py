@@ -81,6 +81,8 @@ SIGNATURES = {
     "supersonic_qwen35_hip_transpose_shd_hsd": [_i, _sz, _sz, _sz, _sz, _p, _p],
     "supersonic_qwen35_hip_sigmoid_mul": [_i, _sz, _sz, _p, _p, _p],
     "supersonic_qwen35_hip_split_qgate": [_i, _sz, _sz, _sz, _sz, _p, _p, _p],
+    "supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled": [_i, _sz, _sz, _i, _i, _i, _p, _p, _p],
+    "supersonic_qwen35_hip_element_add": [_i, _sz, _sz, _p, _p, _p],
     "supersonic_attn_gfx950_decode_workspace_size": [_sz, _sz, _sz, _sz, _sz],
     "supersonic_attn_gfx950_decode":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
@@ -90,6 +92,7 @@ SIGNATURES = {
     "supersonic_attn_gfx950_prefill":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
          _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p],
+    "supersonic_attn_gfx950_o_proj_residual": [_sz, _p, _i, _sz, _sz, _sz, _p, _p, _p],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "supersonic_attn_gfx950_set_profile_events": [_p, _p],
     "supersonic_attn_version": [],
@@ -222,6 +225,17 @@ def split_qgate(ordinal, dtype, s, num_heads, head_dim, src, query_out, gate_out
                                                                    _ptr(src), _ptr(query_out), _ptr(gate_out)))
 
 
+def matmul_rhs_transposed(ordinal, dtype, batch_elems, m, n, k, lhs, rhs, out):
+    """``out[b] = lhs[b] . rhs[b]^T`` (prefill_ffi.rs:2104-2195 binding the tiled bridge)."""
+    _check("matmul_rhs_transposed", load().supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(
+        dtype, ordinal, batch_elems, m, n, k, _ptr(lhs), _ptr(rhs), _ptr(out)))
+
+
+def element_add(ordinal, dtype, total_elems, lhs, rhs, out):
+    _check("element_add", load().supersonic_qwen35_hip_element_add(dtype, ordinal, total_elems, _ptr(lhs),
+                                                                   _ptr(rhs), _ptr(out)))
+
+
 # --------------------------------------------------------------------------
 # Native fused entry points
 # --------------------------------------------------------------------------
@@ -308,6 +322,19 @@ def fused_prefill(ordinal, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table, 
         rotary_dim, S, chunk_start, eps, scale, _ptr(q_proj), _ptr(k_new), _ptr(v_new), _ptr(q_norm_w),
         _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), C.byref(desc), _ptr(out))
     _check("fused_prefill", st)
+
+
+def o_proj_residual(ordinal, attn, o_proj_w, hidden, stream=None):
+    """``hidden = bf16(hidden + bf16(attn . o_proj_w^T))`` in place; hidden bf16 or f32."""
+    import torch
+    rows, attn_dim = attn.shape
+    hidden_dim = o_proj_w.shape[0]
+    assert o_proj_w.shape[1] == attn_dim and tuple(hidden.shape) == (rows, hidden_dim)
+    assert attn.dtype == torch.bfloat16 and o_proj_w.dtype == torch.bfloat16
+    assert attn.is_contiguous() and o_proj_w.is_contiguous() and hidden.is_contiguous()
+    hd = {torch.bfloat16: ScalarType.BF16, torch.float32: ScalarType.F32}[hidden.dtype]
+    _check("o_proj_residual", load().supersonic_attn_gfx950_o_proj_residual(
+        ordinal, _stream_ptr(stream), hd, rows, hidden_dim, attn_dim, _ptr(attn), _ptr(o_proj_w), _ptr(hidden)))
 
 
 def quantize_kv_fp8_ocp(ordinal, src, dst_fp8, dst_scale, num_kv_heads, seq_len, head_dim, max_t, pos_offset,

@@ -8,6 +8,10 @@ torch oracle) and from the reference's own known-answer tests, restated as data:
 * ``config_known_answer.json``: crates/qwen35/src/config.rs:201-259 (head_dim
   256, partial_rotary_factor 0.25 -> rotary_dim 64, rope_theta 1e7, 16 full
   attention layers x 4 kv heads -> kv_bytes_per_token(2) = 65536).
+* ``proj_known_answer.json``: crates/kernel-ffi/src/metal_native.rs:4307-4338
+  (matmul_rhs_transposed), :4430-4469 (matmul + residual), :5807-5827
+  (element_add, bf16), plus a float64 brute-force o_proj + residual case and a
+  case whose answer depends on the reference's two roundings.
 
 Inputs are seeded bf16 values (stored as float lists; every value is exact).
 Run:  python tests/golden/make_golden.py
@@ -126,6 +130,33 @@ def main():
         "q_norm_w": tolist(qw), "k_norm_w": tolist(kw),
         "cache_k": tolist(cache_k), "cache_v": tolist(cache_v),
         "k_rot_expected": tolist(np.array(kh)), "out": out,
+    })
+
+    # Output projection + residual (o_proj row after the gate).
+    kat_lhs = [[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]]
+    kat_rhs = [[1.0, 0.0, 1.0], [0.5, -1.0, 2.0]]
+    m, n, k = 3, 5, 40
+    attn = bf16_randn(rng, m, k)
+    w = bf16_randn(rng, n, k, std=0.2)
+    hid = bf16_randn(rng, m, n)
+    dot = attn.astype(np.float64) @ w.astype(np.float64).T
+    add = brute.bf16_round(dot.astype(np.float32))
+    res = brute.bf16_round((hid.astype(np.float32) + add).astype(np.float32))
+    dump("proj_known_answer.json", {
+        "matmul": {"source": "crates/kernel-ffi/src/metal_native.rs:4307-4338", "lhs": kat_lhs, "rhs": kat_rhs,
+                   "expected": [[4.0, 4.5], [10.0, 9.0]], "tolerance": 0.02},
+        "matmul_residual": {"source": "crates/kernel-ffi/src/metal_native.rs:4430-4469", "lhs": kat_lhs,
+                            "rhs": kat_rhs, "residual": [[0.25, -0.5], [1.0, 2.0]],
+                            "expected": [[4.25, 4.0], [11.0, 11.0]], "tolerance": 0.02},
+        "element_add": {"source": "crates/kernel-ffi/src/metal_native.rs:5807-5827",
+                        "lhs": [1.0, -2.0, 0.5, 10.0], "rhs": [0.25, 3.0, -0.25, -1.5],
+                        "expected": [1.25, 1.0, 0.25, 8.5], "tolerance": 0.02},
+        # hidden 1 + bf16(2^-8 + 2^-20) = 1 + 2^-8, a tie that rounds to even (1.0);
+        # a single rounding of 1 + 2^-8 + 2^-20 would give 1 + 2^-7.
+        "double_rounding": {"attn": [[2.0 ** -8, 2.0 ** -20]], "w": [[1.0, 1.0]], "hidden": [[1.0]],
+                            "expected": [[1.0]], "single_rounding": [[1.0 + 2.0 ** -7]]},
+        "brute": {"attn": tolist(attn), "w": tolist(w), "hidden": tolist(hid), "m": m, "n": n, "k": k,
+                  "expected": tolist(res)},
     })
 
 

@@ -1,0 +1,176 @@
+"""GPU parity of the output projection + residual through the C ABI: the
+drop-in GEMM (`matmul_rhs_transposed_tiled`), the drop-in `element_add` and the
+native `o_proj_residual`.
+
+Bar: every bf16 result is within one bf16 ulp of the oracle's (fp32
+accumulation in a different order can move a rounding by one ulp); with the
+residual, one ulp of the projection plus one ulp of the sum.  Adds are
+bit-exact."""
+import json
+import os
+
+import pytest
+import torch
+
+from gpu_util import DEV, announce, gen
+from oracle import attn_oracle as O
+from supersonic_amd import kernel_ffi as K
+
+pytestmark = pytest.mark.gpu
+G = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "proj_known_answer.json")))
+
+
+def ulp(x):
+    x = x.float().abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(x)) - 7)
+
+
+def assert_ulps(out, ref, slack, name):
+    d = (out.float().cpu() - ref.float()).abs()
+    bad = d > slack
+    assert not bad.any(), f"{name}: {int(bad.sum())} entries off, worst {d.max().item():.3e}"
+
+
+def dropin_matmul(lhs, rhs):
+    batch, m, k = lhs.shape
+    n = rhs.shape[1]
+    out = torch.full((batch, m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    K.matmul_rhs_transposed(0, K.ScalarType.BF16, batch, m, n, k, lhs.to(DEV), rhs.to(DEV), out)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def test_matmul_known_answer():
+    announce("matmul known answer")
+    g = G["matmul"]
+    out = dropin_matmul(torch.tensor([g["lhs"]]).bfloat16(), torch.tensor([g["rhs"]]).bfloat16())
+    assert torch.allclose(out[0].float(), torch.tensor(g["expected"]), atol=g["tolerance"])
+
+
+@pytest.mark.parametrize("batch,m,n,k", [
+    (1, 1, 64, 4096), (1, 8, 4096, 4096), (1, 17, 100, 264), (2, 16, 40, 72), (1, 64, 48, 512),
+    (1, 65, 128, 256), (1, 300, 96, 200), (1, 5, 33, 100), (2, 130, 64, 96),
+])
+def test_matmul_matches_oracle(batch, m, n, k):
+    announce(f"matmul batch={batch} m={m} n={n} k={k}")
+    g = gen(81)
+    lhs = O.randn_bf16(g, batch, m, k)
+    rhs = O.randn_bf16(g, batch, n, k, std=k ** -0.5)
+    out = dropin_matmul(lhs, rhs)
+    ref = O.matmul_rhs_transposed(lhs, rhs)
+    assert_ulps(out, ref, ulp(ref) + 1e-6, "matmul")
+
+
+def test_matmul_empty_k_gives_zeros():
+    out = torch.full((1, 3, 5), 7.0, dtype=torch.bfloat16, device=DEV)
+    K.matmul_rhs_transposed(0, K.ScalarType.BF16, 1, 3, 5, 0, torch.zeros(8, device=DEV),
+                            torch.zeros(8, device=DEV), out)
+    torch.cuda.synchronize()
+    assert torch.all(out == 0)
+
+
+def test_matmul_rejects_other_dtypes():
+    x = torch.zeros(16, device=DEV)
+    with pytest.raises(K.GpuError) as e:
+        K.matmul_rhs_transposed(0, K.ScalarType.F32, 1, 1, 1, 1, x, x, x)
+    assert e.value.status == 272
+
+
+@pytest.mark.parametrize("dtype,tdt", [(K.ScalarType.BF16, torch.bfloat16), (K.ScalarType.F16, torch.float16),
+                                       (K.ScalarType.F32, torch.float32)])
+def test_element_add(dtype, tdt):
+    announce(f"element_add {tdt}")
+    g = G["element_add"]
+    a, b = torch.tensor(g["lhs"]).to(tdt), torch.tensor(g["rhs"]).to(tdt)
+    out = torch.empty_like(a, device=DEV)
+    K.element_add(0, dtype, 4, a.to(DEV), b.to(DEV), out)
+    torch.cuda.synchronize()
+    assert torch.allclose(out.cpu().float(), torch.tensor(g["expected"]), atol=g["tolerance"])
+    gg = gen(82)
+    a = torch.randn(100003, generator=gg).to(tdt)
+    b = torch.randn(100003, generator=gg).to(tdt)
+    out = torch.empty_like(a, device=DEV)
+    K.element_add(0, dtype, a.numel(), a.to(DEV), b.to(DEV), out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), (a.float() + b.float()).to(tdt))
+
+
+def run_o_proj(attn, w, hidden):
+    h = hidden.to(DEV)
+    K.o_proj_residual(0, attn.to(DEV), w.to(DEV), h)
+    torch.cuda.synchronize()
+    return h.cpu()
+
+
+def test_o_proj_known_answer():
+    announce("o_proj known answer")
+    g = G["matmul_residual"]
+    out = run_o_proj(torch.tensor(g["lhs"]).bfloat16(), torch.tensor(g["rhs"]).bfloat16(),
+                     torch.tensor(g["residual"]).bfloat16())
+    assert torch.allclose(out.float(), torch.tensor(g["expected"]), atol=g["tolerance"])
+
+
+@pytest.mark.parametrize("k", [2, 32])
+def test_o_proj_two_roundings(k):
+    """k=2 takes the GEMM path, k=32 the fused kernel: both round the projection first."""
+    g = G["double_rounding"]
+    attn = torch.zeros(1, k)
+    attn[0, :2] = torch.tensor(g["attn"][0])
+    w = torch.zeros(1, k)
+    w[0, :2] = 1.0
+    for dt in (torch.bfloat16, torch.float32):
+        out = run_o_proj(attn.bfloat16(), w.bfloat16(), torch.tensor(g["hidden"]).to(dt))
+        assert out.item() == g["expected"][0][0], (k, dt, out.item())
+
+
+@pytest.mark.parametrize("rows,hidden_dim,attn_dim,max_m", [
+    (8, 4096, 4096, None), (1, 2048, 4096, None), (16, 4096, 4096, None), (64, 256, 1024, None),
+    (33, 300, 520, None), (100, 256, 512, None), (3, 64, 36, None),
+    # the streaming kernel with 2..4 row blocks, and its k split over workgroups
+    (16, 4096, 4096, 64), (33, 300, 520, 64), (64, 256, 1024, 64), (12, 512, 8192, None), (40, 512, 8192, 64),
+])
+@pytest.mark.parametrize("hdt", [torch.bfloat16, torch.float32])
+def test_o_proj_residual_matches_oracle(rows, hidden_dim, attn_dim, max_m, hdt, monkeypatch):
+    announce(f"o_proj rows={rows} hidden={hidden_dim} attn={attn_dim} max_m={max_m} hidden dtype {hdt}")
+    if max_m is not None:
+        monkeypatch.setenv("SUPERSONIC_PROJ_SKINNY_MAX_M", str(max_m))
+    g = gen(83)
+    attn = O.randn_bf16(g, rows, attn_dim)
+    w = O.randn_bf16(g, hidden_dim, attn_dim, std=attn_dim ** -0.5)
+    hidden = O.randn_bf16(g, rows, hidden_dim).to(hdt)
+    out = run_o_proj(attn, w, hidden)
+    add = O.matmul_rhs_transposed(attn, w)
+    ref = O.o_proj_residual(attn, w, hidden)
+    assert out.dtype == hdt
+    assert torch.equal(out.float(), O.bf16r(out.float()))  # f32 hidden keeps bf16 values
+    assert_ulps(out, ref, ulp(add) + ulp(ref) + 1e-6, "o_proj")
+    assert (out.float() == ref).float().mean().item() > 0.95
+
+
+@pytest.mark.parametrize("max_m", [None, "64", "0"])
+def test_o_proj_repeated_calls(max_m, monkeypatch):
+    """Back-to-back calls on one stream, the second smaller: the split-k arrival
+    counters return to zero and the shared workspace carries nothing over."""
+    announce(f"o_proj repeated calls max_m={max_m}")
+    if max_m is not None:
+        monkeypatch.setenv("SUPERSONIC_PROJ_SKINNY_MAX_M", max_m)
+    g = gen(84)
+    for rows, hid, adim in [(8, 512, 8192), (8, 512, 8192), (5, 256, 4096)]:
+        attn = O.randn_bf16(g, rows, adim)
+        w = O.randn_bf16(g, hid, adim, std=adim ** -0.5)
+        hidden = O.randn_bf16(g, rows, hid)
+        out = run_o_proj(attn, w, hidden)
+        ref = O.o_proj_residual(attn, w, hidden)
+        assert_ulps(out, ref, ulp(O.matmul_rhs_transposed(attn, w)) + ulp(ref) + 1e-6, f"o_proj {rows}x{hid}")
+
+
+@pytest.mark.parametrize("max_m", ["64", "0"])
+def test_matmul_batched_paths(max_m, monkeypatch):
+    announce(f"matmul batched max_m={max_m}")
+    monkeypatch.setenv("SUPERSONIC_PROJ_SKINNY_MAX_M", max_m)
+    g = gen(85)
+    lhs = O.randn_bf16(g, 3, 20, 512)
+    rhs = O.randn_bf16(g, 3, 72, 512, std=512 ** -0.5)
+    out = dropin_matmul(lhs, rhs)
+    ref = O.matmul_rhs_transposed(lhs, rhs)
+    assert_ulps(out, ref, ulp(ref) + 1e-6, "batched matmul")
