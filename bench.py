@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
-    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|oproj|copy")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|qkv|oproj|copy")
     return ap.parse_args()
 
 
@@ -105,7 +105,7 @@ def main():
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
         out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "fp8", "mixed",
-                                                          "oproj")}
+                                                          "qkv", "oproj")}
     print(json.dumps(out))
 
 
@@ -337,6 +337,34 @@ class Workloads:
                 "kernel_ms": kern_ms, "bytes": kern_bytes,
                 "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "skinny_kernel",
+                             "bytes_per_launch": kern_bytes}}
+
+    def qkv(self):
+        """Input norm + Q/K/V projections of a config-2 decode step: 8 rows,
+        hidden 4096 -> q_proj 16x2x256 = 8192, k/v 4x256 = 1024 each, bf16
+        weights (84 MB; 4 copies rotate past the 256 MB last-level cache)."""
+        torch, K = self.torch, self.K
+        rows, hid, nq, nkv, copies = 8, 4096, 8192, 1024, 4
+        ws = [[(self.randn(n, hid, seed=60 + 3 * c + i) * (hid ** -0.5)).to(torch.bfloat16).contiguous()
+               for i, n in enumerate((nq, nkv, nkv))] for c in range(copies)]
+        hidden = self.randn(rows, hid, seed=70)
+        nw = self.randn(hid, seed=71) * 0.1
+        outs = [torch.empty(rows, n, dtype=torch.bfloat16, device=self.dev) for n in (nq, nkv, nkv)]
+
+        nwb = nw.to(torch.bfloat16)
+
+        def step(i):
+            K.qkv_proj(0, hidden, nwb, *ws[i], *outs)
+        step_ms, kern_ms, _ = self.timed(step, copies)
+        kern_bytes = (nq + 2 * nkv) * hid * 2 + rows * hid * 2 + hid * 2 + rows * (nq + 2 * nkv) * 2
+        ach = kern_bytes / (kern_ms * 1e-3) / 1e9
+        del ws
+        torch.cuda.empty_cache()
+        return {"workload": "input norm + Q/K/V projections, 8 rows, 4096 -> 8192 + 2x1024, bf16",
+                "ms_per_step": step_ms, "kernel_ms": kern_ms, "bytes": kern_bytes,
+                "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                             "kernel": "input_norm_kernel + skinny_kernel (3 segments), events around both",
                              "bytes_per_launch": kern_bytes}}
 
     def copy(self):

@@ -231,6 +231,27 @@ int supersonic_attn_gfx950_prefill(
     const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
     const supersonic_kv_cache* cache, void* out);
 
+/* Input RMSNorm + Q/K/V projections, before the attention:
+ *   normed = bf16(hidden * rsqrt(mean(hidden^2) + eps) * (1 + input_norm_w))
+ *   q_proj_out = bf16(normed . q_proj_w^T), k_out = bf16(normed . k_proj_w^T),
+ *   v_out = bf16(normed . v_proj_w^T)
+ * hidden [rows, hidden_dim] bf16 (hidden_dtype 2) or f32 holding bf16 values
+ * (hidden_dtype 1); input_norm_w [hidden_dim]; q_proj_w [q_out_dim, hidden_dim],
+ * k/v_proj_w [kv_out_dim, hidden_dim]; outputs [rows, q_out_dim] / [rows,
+ * kv_out_dim], all bf16 -- the q_proj / k_new / v_new of
+ * supersonic_attn_gfx950_decode (q_out_dim = q_heads * 2 * head_dim).  Replaces
+ * the megakernel's input norm and projections (full_attention_4b.hip:4942-4967,
+ * :5019-5101) and rms_norm_rows_model + matmul_proj of prefill_engine.rs:1951-2117.
+ * A norm kernel writes the normed rows once (library workspace), then rows <= 12
+ * (SUPERSONIC_PROJ_SKINNY_MAX_M) with q/kv_out_dim % 16 == 0 take one
+ * weight-streaming launch over the three matrices; otherwise one hipBLASLt GEMM
+ * per matrix.  hidden_dim % 8 == 0.  Asynchronous on `stream`. */
+int supersonic_attn_gfx950_qkv_proj(
+    size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim,
+    size_t q_out_dim, size_t kv_out_dim, float eps, const void* hidden, const void* input_norm_w,
+    const void* q_proj_w, const void* k_proj_w, const void* v_proj_w, void* q_proj_out,
+    void* k_out, void* v_out);
+
 /* Output projection with the residual add, after the gated attention:
  *   hidden[r, j] = bf16(hidden[r, j] + bf16(sum_c attn[r, c] * o_proj_w[j, c]))
  * attn [rows, attn_dim] bf16 (the fused decode/prefill `out`), o_proj_w

@@ -310,6 +310,16 @@ def o_proj_residual(attn: torch.Tensor, w: torch.Tensor, hidden: torch.Tensor) -
     return element_add(hidden, matmul_rhs_transposed(attn, w))
 
 
+def qkv_proj(hidden: torch.Tensor, norm_w: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor,
+             eps: float = 1e-6):
+    """Input RMSNorm then the Q/K/V projections, each rounded to bf16: decode
+    megakernel (full_attention_4b.hip:4942-4967 norm, :5019-5101 projections into
+    ``proj_buf`` with ``bf16_round_rne_f32_finite``); prefill ``rms_norm_rows_model``
+    + ``matmul_proj`` (prefill_engine.rs:1951-2117).  Returns ``(q_proj, k, v)``."""
+    normed = rms_norm_rows(hidden, norm_w, eps)
+    return matmul_rhs_transposed(normed, wq), matmul_rhs_transposed(normed, wk), matmul_rhs_transposed(normed, wv)
+
+
 def randn_bf16(gen: torch.Generator, *shape, std: float = 1.0, mean: float = 0.0) -> torch.Tensor:
     return (torch.randn(*shape, generator=gen, dtype=F32) * std + mean).to(BF16)
 

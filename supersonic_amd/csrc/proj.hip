@@ -34,14 +34,18 @@
 
 namespace ssa {
 
+// Up to three weight matrices side by side in one column space (the Q/K/V
+// projections); segment i holds column blocks [cb_end[i-1], cb_end[i]).
 struct SkinnyParams {
     const uint16_t* x;    // [batch][m][k] bf16
-    const uint16_t* w;    // [batch][n][k] bf16
-    void* out;            // [batch][m][n] (OT)
-    const void* res;      // residual [batch][m][n] (OT), may alias out
+    const uint16_t* w[3]; // [batch][n_i][k] bf16
+    void* out[3];         // [batch][m][n_i] (OT)
+    const void* res;      // residual [batch][m][n_0] (OT), may alias out[0] (one segment)
+    int n_seg[3];
+    int cb_end[3];
     float* part;          // split k: [batch * column blocks][ks_count][MB*16*64] partial sums
     unsigned* arrivals;   // split k: [batch * column blocks] counters, zero between calls
-    int m, n, k;
+    int m, k;
     int ks_count, slice;  // k split over ks_count workgroups of `slice` 32-wide k-steps
     int64_t x_bs, w_bs, o_bs;  // batch strides in elements
 };
@@ -58,12 +62,13 @@ constexpr size_t kSkinnyArrivalBytes = 64 << 10;  // counters at a fixed offset,
 __device__ __forceinline__ bf16x8_v as_bf16x8(const u32x4_v& v) { return __builtin_bit_cast(bf16x8_v, v); }
 
 template <typename OT, bool RES>
-__device__ __forceinline__ void skinny_store(const SkinnyParams& p, int b, int row, int col, float s) {
-    if (row >= p.m || col >= p.n) return;
+__device__ __forceinline__ void skinny_store(const SkinnyParams& p, int seg, int b, int row, int col, float s) {
+    const int n = p.n_seg[seg];
+    if (row >= p.m || col >= n) return;
     float y = bf16_round(s);
-    const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * p.n + col;
+    const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * n + col;
     if constexpr (RES) y = bf16_round(load_f32<OT>(static_cast<const OT*>(p.res), o) + y);
-    store_f32<OT>(static_cast<OT*>(p.out), o, y);
+    store_f32<OT>(static_cast<OT*>(p.out[seg]), o, y);
 }
 
 // Workgroup (column block cb, k slice ks, batch b): 64 W rows x `slice` k-steps.
@@ -80,8 +85,11 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_kernel(SkinnyParams 
     const int wave = tid >> 6;
     const int cbw = wave % kSkinnyCB, kh = wave / kSkinnyCB;
     const int cb = blockIdx.x, ks = blockIdx.y, b = blockIdx.z;
+    const int seg = cb < p.cb_end[0] ? 0 : (cb < p.cb_end[1] ? 1 : 2);
+    const int cbs = cb - (seg ? p.cb_end[seg - 1] : 0);  // column block inside the segment
+    const int n = p.n_seg[seg];
     const uint16_t* x = p.x + b * p.x_bs;
-    const uint16_t* w = p.w + b * p.w_bs;
+    const uint16_t* w = p.w[seg] + b * p.w_bs;
     const int T = (p.k + 31) / 32;
     const int sb0 = ks * p.slice;
     const int sb1 = min(sb0 + p.slice, T);
@@ -90,9 +98,9 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_kernel(SkinnyParams 
     const int s1 = min(s0 + half, sb1);
     const int col = lane & 15;
     const int kq = (lane >> 4) * 8;
-    const int n_w = cb * kSkinnyCols + cbw * 16 + col;
-    const bool nvalid = n_w < p.n;
-    const uint16_t* wrow = w + static_cast<int64_t>(min(n_w, p.n - 1)) * p.k + kq;
+    const int n_w = cbs * kSkinnyCols + cbw * 16 + col;
+    const bool nvalid = n_w < n;
+    const uint16_t* wrow = w + static_cast<int64_t>(min(n_w, n - 1)) * p.k + kq;
     const uint16_t* xrow[MB];
     bool mvalid[MB];
 #pragma unroll
@@ -143,7 +151,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_kernel(SkinnyParams 
         if (split)
             store_agent(p.part + (blk * p.ks_count + ks) * NE + e, sum);
         else
-            skinny_store<OT, RES>(p, b, mb * 16 + (r >> 4), cb * kSkinnyCols + c * 16 + (r & 15), sum);
+            skinny_store<OT, RES>(p, seg, b, mb * 16 + (r >> 4), cbs * kSkinnyCols + c * 16 + (r & 15), sum);
     }
     if (!split) return;
     // The last workgroup of the column block to arrive adds the k slices in
@@ -158,9 +166,83 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_kernel(SkinnyParams 
         const int c = e / (MB * 256), mb = (e / 256) % MB, r = e & 255;
         float sum = 0.f;
         for (int q = 0; q < p.ks_count; ++q) sum += load_agent(base + q * NE + e);
-        skinny_store<OT, RES>(p, b, mb * 16 + (r >> 4), cb * kSkinnyCols + c * 16 + (r & 15), sum);
+        skinny_store<OT, RES>(p, seg, b, mb * 16 + (r >> 4), cbs * kSkinnyCols + c * 16 + (r & 15), sum);
     }
     if (tid == 0) p.arrivals[blk] = 0u;  // every slice has arrived: ready for the next call
+}
+
+// Input RMSNorm ahead of the Q/K/V projections (decode megakernel
+// full_attention_4b.hip:4942-4967; prefill rms_norm_rows_model):
+// normed = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)): one 256-thread
+// workgroup per row, 8 elements (16 or 32 bytes) per thread and chunk, every
+// chunk's load issued before the reduction (k <= 8192 in one pass of
+// registers; longer rows re-read their chunks from cache).
+template <typename XT>
+__device__ __forceinline__ void load8f(const XT* p, float (&f)[8]);
+template <>
+__device__ __forceinline__ void load8f<bf16_t>(const bf16_t* p, float (&f)[8]) { unpack8<bf16_t>(ld16(p), f); }
+template <>
+__device__ __forceinline__ void load8f<float>(const float* p, float (&f)[8]) {
+    const f32x4_v a = *reinterpret_cast<const f32x4_v*>(p);
+    const f32x4_v b = *reinterpret_cast<const f32x4_v*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[e] = a[e];
+        f[4 + e] = b[e];
+    }
+}
+
+template <typename XT>
+__global__ __launch_bounds__(256) void input_norm_kernel(int rows, int k, float eps, const XT* x, const uint16_t* w,
+                                                         uint16_t* out) {
+    __shared__ float part[4];
+    constexpr int CH = 4;  // chunks of 8 held per thread
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const XT* xr = x + static_cast<int64_t>(row) * k;
+    const int nch = k / 8;
+    float v[CH][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int ch = tid + 256 * c;
+        if (ch < nch) load8f<XT>(xr + 8 * ch, v[c]);
+        else
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[c][e] = 0.f;
+    }
+    for (int ch = tid + 256 * CH; ch < nch; ch += 256) {
+        float f[8];
+        load8f<XT>(xr + 8 * ch, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[c][e] * v[c][e];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    const float inv = rsqrtf((part[0] + part[1] + part[2] + part[3]) / static_cast<float>(k) + eps);
+    uint16_t* orow = out + static_cast<int64_t>(row) * k;
+    for (int ch = tid; ch < nch; ch += 256) {
+        const int c = (ch - tid) / 256;
+        float f[8], g[8];
+        if (c < CH) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = v[c < CH ? c : 0][e];
+        } else {
+            load8f<XT>(xr + 8 * ch, f);
+        }
+        unpack8<bf16_t>(ld16(w + 8 * ch), g);
+        u32x4_v o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = f32_to_bf16_bits(f[2 * e] * inv * (g[2 * e] + 1.0f)) |
+                   (f32_to_bf16_bits(f[2 * e + 1] * inv * (g[2 * e + 1] + 1.0f)) << 16);
+        st16(orow + 8 * ch, o);
+    }
 }
 
 // hidden = bf16(hidden + y) over `total` elements (y bf16).
@@ -177,6 +259,14 @@ __global__ void element_add_kernel(size_t total, const T* lhs, const T* rhs, T* 
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += static_cast<size_t>(gridDim.x) * blockDim.x)
         store_f32<T>(out, i, load_f32<T>(lhs, i) + load_f32<T>(rhs, i));
+}
+
+// One weight matrix as the whole column space.
+inline void one_segment(SkinnyParams& p, const void* w, void* out, int n) {
+    p.w[0] = p.w[1] = p.w[2] = static_cast<const uint16_t*>(w);
+    p.out[0] = p.out[1] = p.out[2] = out;
+    p.n_seg[0] = p.n_seg[1] = p.n_seg[2] = n;
+    p.cb_end[0] = p.cb_end[1] = p.cb_end[2] = (n + kSkinnyCols - 1) / kSkinnyCols;
 }
 
 inline unsigned stride_blocks(size_t n) {
@@ -201,7 +291,7 @@ bool skinny_fits(int m, int k, const void* x, const void* w) {
 // per wave) and launches.  Returns a SUPERSONIC status (0 = ok).
 template <typename OT, bool RES>
 int launch_skinny(int dev, hipStream_t st, int batch, SkinnyParams p) {
-    const int ncb = (p.n + kSkinnyCols - 1) / kSkinnyCols;
+    const int ncb = p.cb_end[2];
     const int T = (p.k + 31) / 32;
     const int MB = (p.m + 15) / 16;
     const int64_t wgs = static_cast<int64_t>(ncb) * batch;
@@ -322,10 +412,8 @@ extern "C" int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(int dtype, s
         if (k <= 0 || skinny_fits(m, k, lhs, rhs)) {
             SkinnyParams p{};
             p.x = static_cast<const uint16_t*>(lhs);
-            p.w = static_cast<const uint16_t*>(rhs);
-            p.out = out;
+            one_segment(p, rhs, out, n);
             p.m = m;
-            p.n = n;
             p.k = k > 0 ? k : 0;
             p.x_bs = static_cast<int64_t>(m) * p.k;
             p.w_bs = static_cast<int64_t>(n) * p.k;
@@ -388,11 +476,9 @@ extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, voi
     if (skinny_fits(m, k, attn, o_proj_w)) {
         SkinnyParams p{};
         p.x = static_cast<const uint16_t*>(attn);
-        p.w = static_cast<const uint16_t*>(o_proj_w);
-        p.out = hidden;
+        one_segment(p, o_proj_w, hidden, n);
         p.res = hidden;
         p.m = m;
-        p.n = n;
         p.k = k;
         const int rc = f32 ? launch_skinny<float, true>(dev, st, 1, p) : launch_skinny<bf16_t, true>(dev, st, 1, p);
         if (rc) return rc;
@@ -413,6 +499,75 @@ extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, voi
             hipLaunchKernelGGL((residual_add_kernel<bf16_t>), grid, blk, 0, st, total,
                                static_cast<const uint16_t*>(y), static_cast<bf16_t*>(hidden));
         if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    }
+    if (ev.after) (void)hipEventRecord(ev.after, st);
+    return 0;
+}
+
+extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stream, int hidden_dtype, size_t rows,
+                                               size_t hidden_dim, size_t q_out_dim, size_t kv_out_dim, float eps,
+                                               const void* hidden, const void* input_norm_w, const void* q_proj_w,
+                                               const void* k_proj_w, const void* v_proj_w, void* q_proj_out,
+                                               void* k_out, void* v_out) {
+    if (hidden_dtype != SUPERSONIC_DTYPE_BF16 && hidden_dtype != SUPERSONIC_DTYPE_F32) return SUPERSONIC_ERR_DTYPE;
+    if (rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || q_out_dim > 0x7FFFFFFF || kv_out_dim > 0x7FFFFFFF)
+        return SUPERSONIC_ERR_RANGE;
+    if (rows == 0) return 0;
+    if (!hidden || !input_norm_w || !q_proj_w || !q_proj_out || (kv_out_dim && (!k_proj_w || !v_proj_w || !k_out || !v_out)))
+        return SUPERSONIC_ERR_NULL;
+    if (hidden_dim == 0 || hidden_dim % 8 != 0) return SUPERSONIC_ERR_RANGE;
+    const int dev = static_cast<int>(device_ordinal);
+    ScopedDevice scoped(dev);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int m = static_cast<int>(rows), k = static_cast<int>(hidden_dim);
+    const int nq = static_cast<int>(q_out_dim), nkv = static_cast<int>(kv_out_dim);
+    const bool f32 = hidden_dtype == SUPERSONIC_DTYPE_F32;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(input_norm_w) |
+                           reinterpret_cast<uintptr_t>(q_proj_w) | reinterpret_cast<uintptr_t>(k_proj_w) |
+                           reinterpret_cast<uintptr_t>(v_proj_w)) & 15) == 0;
+    const ProfileEvents ev = take_profile_events();
+    if (ev.before) (void)hipEventRecord(ev.before, st);
+    // the normed rows go to the workspace once (bf16 [rows, hidden_dim])
+    uint16_t* normed = static_cast<uint16_t*>(device_workspace(dev, static_cast<size_t>(m) * k * 2, kWorkspaceProj));
+    if (!normed) return SUPERSONIC_ERR_WORKSPACE;
+    {
+        const dim3 grid(m), blk(256);
+        if (f32)
+            hipLaunchKernelGGL((input_norm_kernel<float>), grid, blk, 0, st, m, k, eps, static_cast<const float*>(hidden),
+                               static_cast<const uint16_t*>(input_norm_w), normed);
+        else
+            hipLaunchKernelGGL((input_norm_kernel<bf16_t>), grid, blk, 0, st, m, k, eps,
+                               static_cast<const bf16_t*>(hidden), static_cast<const uint16_t*>(input_norm_w), normed);
+        if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    }
+    if (skinny_fits(m, k, normed, q_proj_w) && aligned && nq % kSkinnyCols == 0 && nkv % kSkinnyCols == 0) {
+        // the three matrices as one column space of the weight-streaming kernel
+        SkinnyParams p{};
+        p.x = normed;
+        p.w[0] = static_cast<const uint16_t*>(q_proj_w);
+        p.w[1] = static_cast<const uint16_t*>(k_proj_w);
+        p.w[2] = static_cast<const uint16_t*>(v_proj_w);
+        p.out[0] = q_proj_out;
+        p.out[1] = k_out;
+        p.out[2] = v_out;
+        p.n_seg[0] = nq;
+        p.n_seg[1] = p.n_seg[2] = nkv;
+        p.cb_end[0] = nq / kSkinnyCols;
+        p.cb_end[1] = p.cb_end[0] + nkv / kSkinnyCols;
+        p.cb_end[2] = p.cb_end[1] + nkv / kSkinnyCols;
+        p.m = m;
+        p.k = k;
+        if (p.cb_end[2] > 0)
+            if (const int rc = launch_skinny<bf16_t, false>(dev, st, 1, p)) return rc;
+    } else {
+        // GEMM-sized: one hipBLASLt GEMM per matrix
+        const void* ws[3] = {q_proj_w, k_proj_w, v_proj_w};
+        void* os[3] = {q_proj_out, k_out, v_out};
+        const int ns[3] = {nq, nkv, nkv};
+        for (int i = 0; i < 3; ++i) {
+            if (ns[i] == 0) continue;
+            if (lt_gemm(dev, st, 1, m, ns[i], k, normed, ws[i], os[i]) != 0) return SUPERSONIC_ERR_LAUNCH;
+        }
     }
     if (ev.after) (void)hipEventRecord(ev.after, st);
     return 0;

@@ -93,6 +93,7 @@ SIGNATURES = {
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
          _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p],
     "supersonic_attn_gfx950_o_proj_residual": [_sz, _p, _i, _sz, _sz, _sz, _p, _p, _p],
+    "supersonic_attn_gfx950_qkv_proj": [_sz, _p, _i, _sz, _sz, _sz, _sz, _f, _p, _p, _p, _p, _p, _p, _p, _p],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "supersonic_attn_gfx950_set_profile_events": [_p, _p],
     "supersonic_attn_version": [],
@@ -335,6 +336,24 @@ def o_proj_residual(ordinal, attn, o_proj_w, hidden, stream=None):
     hd = {torch.bfloat16: ScalarType.BF16, torch.float32: ScalarType.F32}[hidden.dtype]
     _check("o_proj_residual", load().supersonic_attn_gfx950_o_proj_residual(
         ordinal, _stream_ptr(stream), hd, rows, hidden_dim, attn_dim, _ptr(attn), _ptr(o_proj_w), _ptr(hidden)))
+
+
+def qkv_proj(ordinal, hidden, input_norm_w, q_proj_w, k_proj_w, v_proj_w, q_proj_out, k_out, v_out, eps=1e-6,
+             stream=None):
+    """Input RMSNorm (1 + w) + Q/K/V projections: the fused decode's q_proj / k_new / v_new."""
+    import torch
+    rows, hid = hidden.shape
+    nq, nkv = q_proj_w.shape[0], k_proj_w.shape[0]
+    assert input_norm_w.shape == (hid,) and q_proj_w.shape[1] == hid and k_proj_w.shape == (nkv, hid)
+    assert v_proj_w.shape == (nkv, hid) and tuple(q_proj_out.shape) == (rows, nq)
+    assert tuple(k_out.shape) == (rows, nkv) and tuple(v_out.shape) == (rows, nkv)
+    for t in (input_norm_w, q_proj_w, k_proj_w, v_proj_w, q_proj_out, k_out, v_out):
+        assert t.dtype == torch.bfloat16 and t.is_contiguous()
+    assert hidden.is_contiguous()
+    hd = {torch.bfloat16: ScalarType.BF16, torch.float32: ScalarType.F32}[hidden.dtype]
+    _check("qkv_proj", load().supersonic_attn_gfx950_qkv_proj(
+        ordinal, _stream_ptr(stream), hd, rows, hid, nq, nkv, eps, _ptr(hidden), _ptr(input_norm_w),
+        _ptr(q_proj_w), _ptr(k_proj_w), _ptr(v_proj_w), _ptr(q_proj_out), _ptr(k_out), _ptr(v_out)))
 
 
 def quantize_kv_fp8_ocp(ordinal, src, dst_fp8, dst_scale, num_kv_heads, seq_len, head_dim, max_t, pos_offset,

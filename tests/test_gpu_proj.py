@@ -174,3 +174,67 @@ def test_matmul_batched_paths(max_m, monkeypatch):
     out = dropin_matmul(lhs, rhs)
     ref = O.matmul_rhs_transposed(lhs, rhs)
     assert_ulps(out, ref, ulp(ref) + 1e-6, "batched matmul")
+
+
+def run_qkv(hidden, nw, wq, wk, wv, eps=1e-6):
+    rows = hidden.shape[0]
+    outs = [torch.full((rows, w.shape[0]), float("nan"), dtype=torch.bfloat16, device=DEV) for w in (wq, wk, wv)]
+    K.qkv_proj(0, hidden.to(DEV), nw.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), *outs, eps=eps)
+    torch.cuda.synchronize()
+    return [o.cpu() for o in outs]
+
+
+@pytest.mark.parametrize("rows,hid,nq,nkv", [
+    (8, 4096, 8192, 1024), (1, 2048, 8192, 512), (16, 1000, 512, 128), (3, 4096, 1024, 256),
+    (40, 1024, 512, 128), (8, 512, 1000, 72),
+])
+@pytest.mark.parametrize("hdt", [torch.bfloat16, torch.float32])
+def test_qkv_proj_matches_oracle(rows, hid, nq, nkv, hdt):
+    """Fused kernel (<= 16 rows, widths % 16) and the norm + hipBLASLt path."""
+    announce(f"qkv_proj rows={rows} hidden={hid} q={nq} kv={nkv} hidden dtype {hdt}")
+    g = gen(86)
+    hidden = O.randn_bf16(g, rows, hid).to(hdt)
+    nw = O.randn_bf16(g, hid, std=0.1)
+    wq, wk, wv = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (nq, nkv, nkv))
+    outs = run_qkv(hidden, nw, wq, wk, wv)
+    refs = O.qkv_proj(hidden.float(), nw, wq, wk, wv)
+    for name, out, ref in zip("qkv", outs, refs):
+        # the normed row may round differently by one bf16 ulp in a few places
+        # (hardware rsqrt), which moves a projection by far less than its ulp
+        assert_ulps(out, ref, 2 * ulp(ref) + 2.0 ** -10, f"qkv {name}")
+        assert (out.float() == ref).float().mean().item() > 0.9, name
+
+
+def test_decode_layer_chain():
+    """qkv_proj -> fused decode -> o_proj + residual on device, against the oracle's
+    chain (config-1 heads, a 4096-wide hidden state, B = 4, 300 cached tokens)."""
+    announce("decode layer chain")
+    g = gen(87)
+    B, Hq, Hkv, D, rot, hid, L = 4, 8, 2, 256, 64, 4096, 300
+    shape = O.LayerShape(Hq, Hkv, D, rot)
+    hidden = O.randn_bf16(g, B, hid)
+    nw = O.randn_bf16(g, hid, std=0.1)
+    wq, wk, wv = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (Hq * 2 * D, Hkv * D, Hkv * D))
+    wo = O.randn_bf16(g, hid, Hq * D, std=(Hq * D) ** -0.5)
+    qw, kw = O.norm_weights(g, D)
+    cos, sin = O.rope_tables(rot, L + 2, 1.0e7)
+    kc = O.randn_bf16(g, B, Hkv, L + 1, D)
+    vc = O.randn_bf16(g, B, Hkv, L + 1, D)
+    pos = torch.tensor([L, L - 7, 100, 1], dtype=torch.int32)
+
+    q_proj, k_new, v_new = (t.to(DEV) for t in run_qkv(hidden, nw, wq, wk, wv))
+    cache = K.KvCache(kc.to(DEV), vc.to(DEV))
+    attn = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    K.fused_decode(0, q_proj, k_new, v_new, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV), cache,
+                   attn, q_heads=Hq, kv_heads=Hkv, head_dim=D, rotary_dim=rot, max_kv_len=L + 1)
+    h = hidden.to(DEV)
+    K.o_proj_residual(0, attn, wo.to(DEV), h)
+    torch.cuda.synchronize()
+
+    rq, rk, rv = O.qkv_proj(hidden, nw, wq, wk, wv)
+    ra = O.decode_layer(shape, rq, rk, rv, qw, kw, cos, sin, pos.tolist(), [kc[b].clone() for b in range(B)],
+                        [vc[b].clone() for b in range(B)])
+    rh = O.o_proj_residual(ra, wo, hidden)
+    d = (h.float().cpu() - rh).abs()
+    assert d.max().item() <= 2e-2 * max(1.0, rh.abs().max().item()) and d.mean().item() <= 2e-3, \
+        f"chain: max {d.max().item():.3e} mean {d.mean().item():.3e}"

@@ -66,3 +66,19 @@ def test_matmul_batched_rhs_and_brute():
         ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(exp), 1e-30))) - 7)
         assert np.all(np.abs(out[b].numpy() - exp) <= ulp)
     assert not torch.equal(out[1], O.matmul_rhs_transposed(lhs[1:], rhs[:1])[0])
+
+
+def test_qkv_proj_against_brute_force():
+    """Input norm (1 + w) then three projections, each entry the float64 dot of
+    the bf16-rounded normed row (brute.rms_norm_row restates the norm in float64)."""
+    gen = torch.Generator().manual_seed(6)
+    hid = O.randn_bf16(gen, 2, 64)
+    nw = O.randn_bf16(gen, 64, std=0.1)
+    wq, wk, wv = (O.randn_bf16(gen, n, 64, std=0.125) for n in (32, 16, 16))
+    q, k, v = O.qkv_proj(hid, nw, wq, wk, wv, 1e-6)
+    for r in range(2):
+        normed = brute.bf16_round(np.array(brute.rms_norm_row(hid[r].float().numpy(), nw.float().numpy(), 1e-6), np.float32))
+        for got, w in ((q, wq), (k, wk), (v, wv)):
+            exp = brute.bf16_round((w.double().numpy() @ normed.astype(np.float64)).astype(np.float32))
+            ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(exp), 1e-30))) - 7)
+            assert np.all(np.abs(got[r].numpy() - exp) <= ulp)
