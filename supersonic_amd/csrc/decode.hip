@@ -109,6 +109,15 @@ __device__ __forceinline__ u32x4_v fp8x8_to_bf16x8(u32x2_v w) {
     return r;
 }
 
+// First of the 8 consecutive dims that lane group g (= lane >> 4) holds in
+// QK^T k-step s, for Q (A operand) and K (B operand) alike: 32 s + 8 g for
+// 16-bit K; for e4m3 K a lane loads 16 dims (16 bytes) at once, so k-steps
+// 2 ss and 2 ss + 1 take the two halves: 64 ss + 16 g + 8 (s & 1).
+template <bool FP8>
+__device__ __forceinline__ constexpr int kdim(int s, int g) {
+    return FP8 ? 64 * (s >> 1) + 16 * g + 8 * (s & 1) : 32 * s + 8 * g;
+}
+
 __device__ __forceinline__ void fp8x8_to_f32(u32x2_v w, float* f) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -389,16 +398,16 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     __shared__ u32x4_v qop_s[KSTEPS * 64];
     if (wave == 0) {
         const int hh = lane & 15;
-        const int dk = 8 * (lane >> 4);
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) {
             u32x4_v w;
+            const int dk = kdim<FP8>(s, lane >> 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 float a = 0.f, c = 0.f;
                 if (hh < G) {
-                    a = smem[hh * D + 32 * s + dk + 2 * j];
-                    c = smem[hh * D + 32 * s + dk + 2 * j + 1];
+                    a = smem[hh * D + dk + 2 * j];
+                    c = smem[hh * D + dk + 2 * j + 1];
                 }
                 w[j] = pack2<QT>(a, c);
             }
@@ -431,7 +440,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     // Block data of one 16-token block, loaded one block ahead (registers).
     struct Blk {
         op_t kb[FP8 ? 1 : KSTEPS];
-        u32x2_v kr8[FP8 ? KSTEPS : 1];   // raw e4m3 K: converted when the block is processed
+        u32x4_v kr8[FP8 ? KSTEPS / 2 : 1];  // raw e4m3 K, 16 dims a load: converted when the block is processed
         u32x4_v vr16[FP8 ? 1 : VINS];
         u32x2_v vr8[FP8 ? VINS : 1];
         float ksc, vsc;
@@ -439,7 +448,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     // Buffer resources bound to the block's live rows (a block lies inside one
     // page): rows past kv_len read as zeros, so every load is one per-lane
     // offset plus a constant, with no per-load clamping.
-    const int k_lane_off = (n_s * D + 8 * (lane >> 4)) * ESZ;
+    const int k_lane_off = n_s * D * ESZ + kdim<FP8>(0, lane >> 4) * ESZ;
     // Cache policy of the K/V loads: nontemporal for the bf16 8-wave kernel
     // (every byte is read once; 6.0 -> 7.1 TB/s for its access pattern on
     // MI355X); the FP8 and 4-wave variants measured faster without it.
@@ -452,14 +461,15 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         const __amdgpu_buffer_rsrc_t kr = uniform_rsrc(kbase + base * ESZ, nvalid * D * ESZ);
         const __amdgpu_buffer_rsrc_t vr = uniform_rsrc(vbase + base * ESZ, nvalid * D * ESZ);
         // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
+        if constexpr (!FP8) {
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            if constexpr (!FP8) {
+            for (int s = 0; s < KSTEPS; ++s)
                 B.kb[s] = as_op<op_t>(__builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * s, 0, kStream)));
-            } else {
-                // raw bytes only: converted when the block is processed
-                B.kr8[s] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane_off + 32 * s, 0, kStream));
-            }
+        } else {
+            // raw bytes only, 16 per lane: converted when the block is processed
+#pragma unroll
+            for (int ss = 0; ss < KSTEPS / 2; ++ss)
+                B.kr8[ss] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * ss, 0, kStream));
         }
         // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
 #pragma unroll
@@ -553,7 +563,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
                 if constexpr (!FP8) x ^= __builtin_bit_cast(u32x4_v, B.kb[s]);
-                else x[s & 3] ^= B.kr8[s][0] ^ B.kr8[s][1];
+                else x ^= B.kr8[s >> 1];
             }
             if constexpr (!FP8) {
 #pragma unroll
@@ -573,7 +583,10 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         } else {
             op_t kb[KSTEPS];
 #pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) kb[s] = as_op<op_t>(fp8x8_to_bf16x8(B.kr8[s]));
+            for (int s = 0; s < KSTEPS; ++s) {
+                const u32x4_v& w = B.kr8[s >> 1];
+                kb[s] = as_op<op_t>(fp8x8_to_bf16x8((s & 1) ? u32x2_v{w[2], w[3]} : u32x2_v{w[0], w[1]}));
+            }
             process(min(16, t_main - t0), kb, B.ksc, B.vsc, vdec);
         }
     };
@@ -614,7 +627,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) {
             u32x4_v w;
-            const int d0 = 32 * s + 8 * (lane >> 4);
+            const int d0 = kdim<FP8>(s, lane >> 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(kn_s[d0 + 2 * j], kn_s[d0 + 2 * j + 1]);
             kbn[s] = as_op<op_t>(w);
