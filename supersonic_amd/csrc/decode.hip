@@ -456,7 +456,11 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     const int v_lane_off = (vt * D + vd) * ESZ;
     auto fetch = [&](int blk, Blk& B) {
         const int t0 = t_begin + blk * 16;
-        const int64_t base = p.kv.row(b, kvh, t0, D);
+        // The page comes through the scalar cache (lgkmcnt): waiting for it
+        // does not wait for the other block's vector loads still in flight.
+        const int ub = __builtin_amdgcn_readfirstlane(b), uk = __builtin_amdgcn_readfirstlane(kvh);
+        const int ut = __builtin_amdgcn_readfirstlane(t0);
+        const int64_t base = p.kv.row_uniform(ub, uk, ut, D);
         const int nvalid = min(16, t_main - t0);
         const __amdgpu_buffer_rsrc_t kr = uniform_rsrc(kbase + base * ESZ, nvalid * D * ESZ);
         const __amdgpu_buffer_rsrc_t vr = uniform_rsrc(vbase + base * ESZ, nvalid * D * ESZ);
@@ -481,7 +485,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         B.ksc = 1.f;
         B.vsc = 1.f;
         if constexpr (FP8) {
-            const int64_t sb = p.kv.srow(b, kvh, t0);
+            const int64_t sb = p.kv.srow_uniform(ub, uk, ut);
             const int kn = min(n_s, nvalid - 1);
             B.ksc = p.kv.ks[sb + kn];
             B.vsc = p.kv.vs[sb + kn];

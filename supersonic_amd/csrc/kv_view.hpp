@@ -45,6 +45,16 @@ struct KvView {
         }
         return b * seq_stride + h * head_stride + static_cast<int64_t>(t) * D;
     }
+    // srow() for a wave-uniform (b, h, t), through the scalar cache as row_uniform().
+    __device__ __forceinline__ int64_t srow_uniform(int b, int h, int t) const {
+        if (bt) {
+            typedef const __attribute__((address_space(4))) int32_t* cptr;
+            const cptr cbt = reinterpret_cast<cptr>(reinterpret_cast<uintptr_t>(bt));
+            const int pg = cbt[static_cast<int64_t>(b) * max_pages + t / page_size];
+            return static_cast<int64_t>(pg) * s_page + h * s_head + (t % page_size);
+        }
+        return b * s_seq + h * s_head + t;
+    }
     // Offset of token t's fp8 scale.
     __device__ __forceinline__ int64_t srow(int b, int h, int t) const {
         if (bt) {
