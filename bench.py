@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
-    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|qkv|oproj|copy")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|qkv|oproj|layer_graph|copy")
     return ap.parse_args()
 
 
@@ -105,7 +105,7 @@ def main():
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
         out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "fp8", "mixed",
-                                                          "qkv", "oproj")}
+                                                          "qkv", "oproj", "layer_graph")}
     print(json.dumps(out))
 
 
@@ -366,6 +366,65 @@ class Workloads:
                              "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                              "kernel": "input_norm_kernel + skinny_kernel (3 segments), events around both",
                              "bytes_per_launch": kern_bytes}}
+
+    def layer_graph(self):
+        """One decode layer (input norm + Q/K/V projections, fused attention step,
+        o_proj + residual) per step, eager launches against a HIP graph replay of
+        the same launches: config 1 heads (B=1, 8/2 heads, 2048 cached tokens,
+        hidden 1024) and config 2 (B=8, 16/4 heads, 32768 cached, hidden 4096)."""
+        torch, K, O = self.torch, self.K, self.O
+        res = {}
+        for name, (B, Hq, Hkv, hid, L) in {"config1": (1, 8, 2, 1024, 2048),
+                                           "config2_b8": (8, 16, 4, 4096, 32768)}.items():
+            D, rot = 256, 64
+            g = torch.Generator().manual_seed(5)
+            hidden0 = self.randn(B, hid, seed=80)
+            nw = (self.randn(hid, seed=81) * 0.1).to(torch.bfloat16)
+            wq, wk, wv = ((self.randn(n, hid, seed=82 + i) * hid ** -0.5).to(torch.bfloat16)
+                          for i, n in enumerate((Hq * 2 * D, Hkv * D, Hkv * D)))
+            wo = (self.randn(hid, Hq * D, seed=85) * (Hq * D) ** -0.5).to(torch.bfloat16)
+            qw, kw = (t.to(self.dev) for t in O.norm_weights(g, D))
+            cos, sin = (t.to(self.dev) for t in O.rope_tables(rot, L + 2, 1.0e7))
+            kc = self.randn(B, Hkv, L + 1, D, seed=86)
+            vc = self.randn(B, Hkv, L + 1, D, seed=87)
+            cache = K.KvCache(kc, vc)
+            pos = torch.full((B,), L, dtype=torch.int32, device=self.dev)
+            q_proj = torch.empty(B, Hq * 2 * D, dtype=torch.bfloat16, device=self.dev)
+            k_new = torch.empty(B, Hkv * D, dtype=torch.bfloat16, device=self.dev)
+            v_new = torch.empty_like(k_new)
+            attn = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=self.dev)
+            hidden = hidden0.clone()
+            st = torch.cuda.Stream()
+
+            def layer():
+                K.qkv_proj(0, hidden, nw, wq, wk, wv, q_proj, k_new, v_new, stream=st)
+                K.fused_decode(0, q_proj, k_new, v_new, qw, kw, cos, sin, pos, cache, attn, q_heads=Hq,
+                               kv_heads=Hkv, head_dim=D, rotary_dim=rot, max_kv_len=L + 1, stream=st)
+                K.o_proj_residual(0, attn, wo, hidden, stream=st)
+
+            def timed_on_stream(fn):
+                with torch.cuda.stream(st):
+                    for _ in range(self.warmup):
+                        fn()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(st)
+                    for _ in range(self.steps):
+                        fn()
+                    e1.record(st)
+                st.synchronize()
+                return e0.elapsed_time(e1) / self.steps
+
+            eager_ms = timed_on_stream(layer)
+            graph = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=st):
+                layer()
+            graph_ms = timed_on_stream(graph.replay)
+            res[name] = {"eager_us_per_layer": round(eager_ms * 1e3, 2), "graph_us_per_layer": round(graph_ms * 1e3, 2),
+                         "launches_per_layer": 4}
+            del kc, vc, cache, graph
+            torch.cuda.empty_cache()
+        return {"workload": "decode layer (qkv_proj + fused decode + o_proj), eager vs HIP graph", **res}
 
     def copy(self):
         """Plain device copy of known size, to calibrate FETCH_SIZE/WRITE_SIZE counters."""

@@ -1,0 +1,129 @@
+"""A whole decode layer (input norm + Q/K/V projections, fused attention step,
+output projection + residual) and a fused prefill chunk captured into a HIP
+graph through torch.cuda.CUDAGraph.  The entry points allocate nothing once
+their workspaces exist and record no memset nodes.  The prefill is
+deterministic, so its replays equal the eager result bit for bit; the decode
+waves claim 16-token blocks dynamically, so the fp32 order of their merge (and
+an occasional bf16 rounding) varies between any two runs, eager or replayed,
+and its replays are held to two bf16 ulps of the eager result.  Replays are
+separated by eager work (the hidden state is reset, outputs are read back)."""
+import pytest
+import torch
+
+from gpu_util import DEV, announce, gen
+from oracle import attn_oracle as O
+from supersonic_amd import kernel_ffi as K
+
+pytestmark = pytest.mark.gpu
+
+
+def decode_layer_inputs(B, Hq, Hkv, D, rot, hid, L, seed):
+    g = gen(seed)
+    d = dict(hidden=O.randn_bf16(g, B, hid), nw=O.randn_bf16(g, hid, std=0.1))
+    d["wq"], d["wk"], d["wv"] = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (Hq * 2 * D, Hkv * D, Hkv * D))
+    d["wo"] = O.randn_bf16(g, hid, Hq * D, std=(Hq * D) ** -0.5)
+    d["qw"], d["kw"] = O.norm_weights(g, D)
+    d["cos"], d["sin"] = O.rope_tables(rot, L + 2, 1.0e7)
+    d["kc"] = O.randn_bf16(g, B, Hkv, L + 1, D)
+    d["vc"] = O.randn_bf16(g, B, Hkv, L + 1, D)
+    return {k: v.to(DEV) for k, v in d.items()}
+
+
+def make_layer(B, Hq, Hkv, D, rot, hid, L, seed, stream):
+    d = decode_layer_inputs(B, Hq, Hkv, D, rot, hid, L, seed)
+    pos = torch.tensor([L - 3 * b for b in range(B)], dtype=torch.int32, device=DEV)
+    cache = K.KvCache(d["kc"], d["vc"])
+    q_proj = torch.empty(B, Hq * 2 * D, dtype=torch.bfloat16, device=DEV)
+    k_new = torch.empty(B, Hkv * D, dtype=torch.bfloat16, device=DEV)
+    v_new = torch.empty_like(k_new)
+    attn = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    hidden = d["hidden"].clone()
+
+    def layer():
+        K.qkv_proj(0, hidden, d["nw"], d["wq"], d["wk"], d["wv"], q_proj, k_new, v_new, stream=stream)
+        K.fused_decode(0, q_proj, k_new, v_new, d["qw"], d["kw"], d["cos"], d["sin"], pos, cache, attn,
+                       q_heads=Hq, kv_heads=Hkv, head_dim=D, rotary_dim=rot, max_kv_len=L + 1, stream=stream)
+        K.o_proj_residual(0, attn, d["wo"], hidden, stream=stream)
+    return layer, hidden, d["hidden"], attn
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,hid,L", [(1, 8, 2, 1024, 2048), (8, 16, 4, 4096, 4000)])
+def test_decode_layer_graph_replays_match_eager(B, Hq, Hkv, hid, L):
+    announce(f"decode layer graph B={B} Hq={Hq} Hkv={Hkv} hidden={hid} L={L}")
+    s = torch.cuda.Stream()
+    layer, hidden, hidden0, attn = make_layer(B, Hq, Hkv, 256, 64, hid, L, 91, s)
+    with torch.cuda.stream(s):
+        layer()  # eager: workspaces are allocated here, before the capture
+    s.synchronize()
+    eager_h, eager_a = hidden.clone(), attn.clone()
+    g = torch.cuda.CUDAGraph()
+    hidden.copy_(hidden0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        layer()
+    for r in range(3):
+        hidden.copy_(hidden0)
+        attn.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close_ulps(attn, eager_a, f"replay {r}: attention")
+        # a near-zero residual sum has a small ulp: the floor is the projection's scale
+        assert_close_ulps(hidden, eager_h, f"replay {r}: hidden", floor=2.0 ** -6)
+
+
+def assert_close_ulps(out, ref, name, floor=0.0):
+    x, y = out.float(), ref.float()
+    ulp = torch.exp2(torch.floor(torch.log2(y.abs().clamp_min(2.0 ** -100))) - 7)
+    bad = (x - y).abs() > 2 * ulp + floor
+    assert not bad.any(), f"{name}: {int(bad.sum())} entries beyond 2 ulps, max diff {(x - y).abs().max().item():.3e}"
+    assert (x == y).float().mean().item() > 0.9, f"{name}: too few identical entries"
+
+
+def test_decode_eager_runs_agree_to_ulps():
+    """Two eager runs of the same step: the dynamic block claiming changes only
+    the fp32 summation order."""
+    announce("decode eager repeat")
+    s = torch.cuda.Stream()
+    layer, hidden, hidden0, attn = make_layer(8, 16, 4, 256, 64, 4096, 4000, 93, s)
+    outs = []
+    for _ in range(2):
+        hidden.copy_(hidden0)
+        with torch.cuda.stream(s):
+            layer()
+        s.synchronize()
+        outs.append(attn.clone())
+    assert_close_ulps(outs[1], outs[0], "eager repeat")
+
+
+def test_prefill_graph_replays_match_eager():
+    announce("prefill graph")
+    S, Hq, Hkv, D, rot, start = 300, 16, 4, 256, 64, 200
+    g0 = gen(92)
+    qp = O.randn_bf16(g0, S, Hq * 2 * D).to(DEV)
+    kr = O.randn_bf16(g0, S, Hkv * D).to(DEV)
+    vr = O.randn_bf16(g0, S, Hkv * D).to(DEV)
+    qw, kw = (t.to(DEV) for t in O.norm_weights(g0, D))
+    cos, sin = (t.to(DEV) for t in O.rope_tables(rot, start + S + 1, 1.0e7))
+    kc = O.randn_bf16(g0, 1, Hkv, start + S, D).to(DEV)
+    vc = O.randn_bf16(g0, 1, Hkv, start + S, D).to(DEV)
+    cache = K.KvCache(kc, vc)
+    out = torch.empty(S, Hq * D, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+
+    def step():
+        K.fused_prefill(0, qp, kr, vr, qw, kw, cos, sin, cache, out, q_heads=Hq, kv_heads=Hkv, head_dim=D,
+                        rotary_dim=rot, chunk_start=start, stream=s)
+    with torch.cuda.stream(s):
+        step()
+    s.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    for r in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
