@@ -140,7 +140,7 @@ int supersonic_qwen35_hip_split_qgate(
  * rhs [batch, n, k], out [batch, m, n], bf16 only (the projections, o_proj
  * included, of prefill_engine.rs:356-414).  Replaces
  * kernels/full_attention_bridge_4b.cpp:3683-3704 (kernel full_attention_4b.hip:2513-2575),
- * bound at prefill_ffi.rs:782-792.  m <= 64: HBM-streaming MFMA kernel; larger m:
+ * bound at prefill_ffi.rs:782-792.  m <= 12 (SUPERSONIC_PROJ_SKINNY_MAX_M): HBM-streaming MFMA kernel; larger m:
  * hipBLASLt.  Status: 272 bad dtype, 270 launch, 271 sync. */
 int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(
     int dtype, size_t device_ordinal, size_t batch_elems, int m, int n, int k,
@@ -245,7 +245,9 @@ int supersonic_attn_gfx950_prefill(
  * A norm kernel writes the normed rows once (library workspace), then rows <= 12
  * (SUPERSONIC_PROJ_SKINNY_MAX_M) with q/kv_out_dim % 16 == 0 take one
  * weight-streaming launch over the three matrices; otherwise one hipBLASLt GEMM
- * per matrix.  hidden_dim % 8 == 0.  Asynchronous on `stream`. */
+ * per matrix.  hidden_dim % 8 == 0.  Asynchronous on `stream`.  The normed rows
+ * live in a library workspace per device: calls that overlap on one device
+ * (different streams) race. */
 int supersonic_attn_gfx950_qkv_proj(
     size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim,
     size_t q_out_dim, size_t kv_out_dim, float eps, const void* hidden, const void* input_norm_w,
@@ -259,9 +261,11 @@ int supersonic_attn_gfx950_qkv_proj(
  * (hidden_dtype 2, the prefill engine's hidden) or f32 holding bf16 values
  * (hidden_dtype 1, the megakernel's hidden_f32).  Replaces the megakernel's
  * step G (full_attention_4b.hip:5481-5577) and matmul_proj + residual_add of
- * prefill_engine.rs:2308-2334.  rows <= 64 with attn_dim % 8 == 0: one
+ * prefill_engine.rs:2308-2334.  rows <= 12 (SUPERSONIC_PROJ_SKINNY_MAX_M, at most 64) with attn_dim % 8 == 0: one
  * HBM-streaming MFMA kernel with the residual fused; otherwise hipBLASLt and a
- * residual kernel.  Asynchronous on `stream`. */
+ * residual kernel.  Asynchronous on `stream`.  Split-k partials, arrival
+ * counters and the GEMM output live in library workspaces per device: calls
+ * that overlap on one device (different streams) race. */
 int supersonic_attn_gfx950_o_proj_residual(
     size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim,
     size_t attn_dim, const void* attn, const void* o_proj_w, void* hidden);
