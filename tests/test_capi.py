@@ -61,6 +61,9 @@ def test_version(lib):
     ("supersonic_qwen35_hip_transpose_shd_hsd", (5, 0, 1, 1, 1, None, None), 320),
     ("supersonic_qwen35_hip_sigmoid_mul", (5, 0, 1, None, None, None), 350),
     ("supersonic_qwen35_hip_split_qgate", (5, 0, 1, 1, 1, None, None, None), 370),
+    ("supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled", (1, 0, 1, 1, 1, 8, None, None, None), 272),
+    ("supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled", (0, 0, 1, 1, 1, 8, None, None, None), 272),
+    ("supersonic_qwen35_hip_element_add", (5, 0, 1, None, None, None), 300),
 ])
 def test_validation_status_codes(lib, fn, args, code):
     assert getattr(lib, fn)(*args) == code
@@ -92,6 +95,24 @@ def test_fused_entry_validation(lib):
     att = lambda kvd: lib.supersonic_attn_gfx950_decode_attend(0, None, kvd, 1, 8, 2, 256, 16, 0.0625, None, p,
                                                                C.byref(desc), None, p, None, 0)
     assert att(2) == K.ERR["NULL"]
+
+
+def test_projection_entry_validation(lib):
+    p = 0x1000  # never dereferenced: validation fails first
+    op = lambda hd, rows, hid, adim, attn=p, w=p, h=p: lib.supersonic_attn_gfx950_o_proj_residual(
+        0, None, hd, rows, hid, adim, attn, w, h)
+    assert op(0, 8, 64, 64) == K.ERR["DTYPE"]          # f16 hidden is not a reference layout
+    assert op(2, 8, 64, 64, h=None) == K.ERR["NULL"]
+    assert op(1, 8, 64, 64, w=None) == K.ERR["NULL"]
+    assert op(2, 1 << 31, 64, 64) == K.ERR["RANGE"]
+    assert op(2, 0, 64, 64, attn=None, w=None, h=None) == 0  # nothing to do
+    qkv = lambda hd, hid, nq=64, nkv=16, x=p, kw=p: lib.supersonic_attn_gfx950_qkv_proj(
+        0, None, hd, 4, hid, nq, nkv, 1e-6, x, p, p, kw, p, p, p, p)
+    assert qkv(0, 64) == K.ERR["DTYPE"]
+    assert qkv(2, 64, x=None) == K.ERR["NULL"]
+    assert qkv(1, 64, kw=None) == K.ERR["NULL"]
+    assert qkv(2, 60) == K.ERR["RANGE"]                # rows are read 16 bytes at a time
+    assert qkv(2, 0) == K.ERR["RANGE"]
 
 
 def test_workspace_size_is_host_only(lib):
