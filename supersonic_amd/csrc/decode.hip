@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -729,25 +730,34 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     __syncthreads();
     SSA_DSTAMP(4);
     if (!last_s) return;
-    for (int hh = wave; hh < G; hh += NW) {
+    // One online pass over the splits of each head, MCH at a time with all
+    // their loads in flight together.  With at least twice as many waves as
+    // heads, two waves share a head (half its dims each) and take 32 splits a
+    // round.  The gate is loaded before the partials, so its round trip is
+    // not the last one.
+    auto merge_head = [&](const int hh, const int part, auto mch_tag, auto dpw_tag) {
+        constexpr int MCH = decltype(mch_tag)::value;
+        constexpr int DPW = decltype(dpw_tag)::value;  // dims per lane handled by this wave
         const int h = kvh * G + hh;
         const int64_t row0 = pre_b * p.Hq + static_cast<int64_t>(h) * n_b;
-        // One online pass over the splits, MCH at a time with all their loads
-        // in flight together (a handful of round trips instead of one per split).
-        constexpr int DPL = D / 64;  // dims per lane
-        constexpr int MCH = 16;
-        float M = -1e30f, Ls = 0.f, o[DPL];
+        float gv[DPW];
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) o[k] = 0.f;
+        for (int k = 0; k < DPW; ++k)
+            gv[k] = p.gate ? bf16_bits_to_f32(p.gate[b * p.g_bstride + h * p.g_hstride + lane + 64 * (part * DPW + k)])
+                           : 0.f;
+        float M = -1e30f, Ls = 0.f, o[DPW];
+#pragma unroll
+        for (int k = 0; k < DPW; ++k) o[k] = 0.f;
         for (int s0 = 0; s0 < ns; s0 += MCH) {
-            float ms[MCH], ls[MCH], os[MCH][DPL];
+            float ms[MCH], ls[MCH], os[MCH][DPW];
 #pragma unroll
             for (int c = 0; c < MCH; ++c) {
                 const int sc = min(s0 + c, ns - 1);  // duplicates past ns get zero weight below
                 ms[c] = load_agent(&p.part_ml[2 * (row0 + sc)]);
                 ls[c] = load_agent(&p.part_ml[2 * (row0 + sc) + 1]);
 #pragma unroll
-                for (int k = 0; k < DPL; ++k) os[c][k] = load_agent(&p.part_o[(row0 + sc) * D + lane + 64 * k]);
+                for (int k = 0; k < DPW; ++k)
+                    os[c][k] = load_agent(&p.part_o[(row0 + sc) * D + lane + 64 * (part * DPW + k)]);
             }
             float mc = M;
 #pragma unroll
@@ -756,28 +766,40 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
             const float a = __builtin_amdgcn_exp2f(M - mc);
             Ls *= a;
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) o[k] *= a;
+            for (int k = 0; k < DPW; ++k) o[k] *= a;
 #pragma unroll
             for (int c = 0; c < MCH; ++c) {
                 const float f = s0 + c < ns ? __builtin_amdgcn_exp2f(ms[c] - mc) : 0.f;
                 Ls = fmaf(f, ls[c], Ls);
 #pragma unroll
-                for (int k = 0; k < DPL; ++k) o[k] = fmaf(f, os[c][k], o[k]);
+                for (int k = 0; k < DPW; ++k) o[k] = fmaf(f, os[c][k], o[k]);
             }
             M = mc;
         }
         const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) {
-            const int d = lane + 64 * k;
+        for (int k = 0; k < DPW; ++k) {
+            const int d = lane + 64 * (part * DPW + k);
             float r = o[k] * inv;
             if (p.gate) {
                 // bf16(bf16(attn) * sigmoid(gate)) (full_attention_4b.hip:5464-5470)
-                const float g = bf16_bits_to_f32(p.gate[b * p.g_bstride + h * p.g_hstride + d]);
-                r = bf16_round(bf16_round(r) * (1.0f / (1.0f + expf(-g))));
+                r = bf16_round(bf16_round(r) * (1.0f / (1.0f + expf(-gv[k]))));
             }
             store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + d, r);
         }
+    };
+    constexpr int DPL = D / 64;  // dims per lane of a whole head
+    if constexpr (DPL % 2 == 0) {
+        if (2 * G <= NW) {
+            if (wave < 2 * G)
+                merge_head(wave >> 1, wave & 1, std::integral_constant<int, 32>{}, std::integral_constant<int, DPL / 2>{});
+        } else {
+            for (int hh = wave; hh < G; hh += NW)
+                merge_head(hh, 0, std::integral_constant<int, 16>{}, std::integral_constant<int, DPL>{});
+        }
+    } else {
+        for (int hh = wave; hh < G; hh += NW)
+            merge_head(hh, 0, std::integral_constant<int, 16>{}, std::integral_constant<int, DPL>{});
     }
     SSA_DSTAMP(5);
     if (tid == 0) p.arrivals[b * p.Hkv + kvh] = 0u;  // every split has arrived: ready for the next call
