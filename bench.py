@@ -35,7 +35,7 @@ TRAFFIC_JSON = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
 def measured_traffic(workload: str):
     """HBM bytes per launch of the workload's dominant kernel, from the
     committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (calibrated against a
-    plain copy; profiles/traffic_pmc_decode_prefill.md holds the commands), or
+    plain copy; profiles/hbm_traffic_pmc.md holds the commands), or
     None when no measurement is on file."""
     try:
         with open(TRAFFIC_JSON) as f:
@@ -336,7 +336,8 @@ class Workloads:
         return {"workload": "o_proj + residual, 8 rows, 4096 -> 4096, bf16", "ms_per_step": step_ms,
                 "kernel_ms": kern_ms, "bytes": kern_bytes,
                 "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "skinny_kernel",
+                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic("oproj"),
+                             "kernel": "skinny_kernel",
                              "bytes_per_launch": kern_bytes}}
 
     def qkv(self):
@@ -363,7 +364,8 @@ class Workloads:
         return {"workload": "input norm + Q/K/V projections, 8 rows, 4096 -> 8192 + 2x1024, bf16",
                 "ms_per_step": step_ms, "kernel_ms": kern_ms, "bytes": kern_bytes,
                 "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                             "frac": round(ach / HBM_PEAK_GBS, 4),
+                             "traffic": measured_traffic("qkv"),  # skinny_kernel's bytes (the norm kernel: 64 KB)
                              "kernel": "input_norm_kernel + skinny_kernel (3 segments), events around both",
                              "bytes_per_launch": kern_bytes}}
 
