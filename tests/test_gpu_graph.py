@@ -4,8 +4,10 @@ graph through torch.cuda.CUDAGraph.  The entry points allocate nothing once
 their workspaces exist and record no memset nodes.  The prefill is
 deterministic, so its replays equal the eager result bit for bit; the decode
 waves claim 16-token blocks dynamically, so the fp32 order of their merge (and
-an occasional bf16 rounding) varies between any two runs, eager or replayed,
-and its replays are held to two bf16 ulps of the eager result.  Replays are
+an occasional bf16 rounding) varies between any two runs, eager or replayed:
+its replays are held to two bf16 ulps of the eager result plus an absolute
+2^-8 (entries near zero come from cancellation, and their own ulp is far
+below the summation-order error of the terms).  Replays are
 separated by eager work (the hidden state is reset, outputs are read back)."""
 import pytest
 import torch
@@ -67,7 +69,7 @@ def test_decode_layer_graph_replays_match_eager(B, Hq, Hkv, hid, L):
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
-        assert_close_ulps(attn, eager_a, f"replay {r}: attention")
+        assert_close_ulps(attn, eager_a, f"replay {r}: attention", floor=2.0 ** -8)
         # a near-zero residual sum has a small ulp: the floor is the projection's scale
         assert_close_ulps(hidden, eager_h, f"replay {r}: hidden", floor=2.0 ** -6)
 
@@ -93,7 +95,7 @@ def test_decode_eager_runs_agree_to_ulps():
             layer()
         s.synchronize()
         outs.append(attn.clone())
-    assert_close_ulps(outs[1], outs[0], "eager repeat")
+    assert_close_ulps(outs[1], outs[0], "eager repeat", floor=2.0 ** -8)
 
 
 def test_prefill_graph_replays_match_eager():
