@@ -337,7 +337,7 @@ class Workloads:
                 "kernel_ms": kern_ms, "bytes": kern_bytes,
                 "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic("oproj"),
-                             "kernel": "skinny_kernel",
+                             "kernel": "skinny_lds_kernel",
                              "bytes_per_launch": kern_bytes}}
 
     def qkv(self):
@@ -365,8 +365,8 @@ class Workloads:
                 "ms_per_step": step_ms, "kernel_ms": kern_ms, "bytes": kern_bytes,
                 "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(ach / HBM_PEAK_GBS, 4),
-                             "traffic": measured_traffic("qkv"),  # skinny_kernel's bytes (the norm kernel: 64 KB)
-                             "kernel": "input_norm_kernel + skinny_kernel (3 segments), events around both",
+                             "traffic": measured_traffic("qkv"),  # the projection kernel's bytes (the norm kernel: 128 KB)
+                             "kernel": "input_norm_kernel + skinny_lds_kernel (3 segments), events around both",
                              "bytes_per_launch": kern_bytes}}
 
     def layer_graph(self):
