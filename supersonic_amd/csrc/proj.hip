@@ -266,7 +266,7 @@ constexpr int kXsMax = 32768;  // staged elements (64 KB): two workgroups per CU
 constexpr int kXsChunks = kXsMax / 8 / 512;  // 16-byte chunks per thread at most
 
 struct SkinnyLdsParams {
-    const void* x;          // [batch][m][k] XT
+    const uint16_t* x;      // [batch][m][k] bf16
     const uint16_t* w[3];
     void* out[3];
     const void* res;
@@ -280,23 +280,7 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <typename XT>
-__device__ __forceinline__ u32x4_v load_bf16x8(const XT* p);
-template <>
-__device__ __forceinline__ u32x4_v load_bf16x8<bf16_t>(const bf16_t* p) { return ld16(p); }
-template <>
-__device__ __forceinline__ u32x4_v load_bf16x8<float>(const float* p) {
-    // f32 rows hold bf16 values (the megakernel rounds its hidden state at
-    // every layer start): the packing is exact
-    const f32x4_v a = *reinterpret_cast<const f32x4_v*>(p);
-    const f32x4_v b = *reinterpret_cast<const f32x4_v*>(p + 4);
-    return u32x4_v{f32_to_bf16_bits(a[0]) | (f32_to_bf16_bits(a[1]) << 16),
-                   f32_to_bf16_bits(a[2]) | (f32_to_bf16_bits(a[3]) << 16),
-                   f32_to_bf16_bits(b[0]) | (f32_to_bf16_bits(b[1]) << 16),
-                   f32_to_bf16_bits(b[2]) | (f32_to_bf16_bits(b[3]) << 16)};
-}
-
-template <typename XT, typename OT, bool RES>
+template <typename OT, bool RES>
 __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_eu(4))) void skinny_lds_kernel(SkinnyLdsParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[kXsMax + 16 * 8];
     __shared__ __attribute__((aligned(16))) float red[kSkinnyWaves][256];
@@ -310,7 +294,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_
     const int k = p.k, m = p.m;
     const int ldx = k + 8;  // padded LDS row: the 16 rows of an A operand read hit distinct banks
     const int cpr = k / 8;  // 16-byte chunks per row
-    const XT* x = static_cast<const XT*>(p.x) + b * p.x_bs;
+    const uint16_t* x = p.x + b * p.x_bs;
     const u32x4_v zero = {0u, 0u, 0u, 0u};
 
     // 1. the activation rows (and norm weights), ahead of any W load
@@ -322,7 +306,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int j = 0; j < kXsChunks; ++j) {
         const int c = min(tid + 512 * j, nch - 1);
-        xr[j] = load_bf16x8<XT>(x + static_cast<int64_t>(c / cpr) * k + 8 * (c % cpr));
+        xr[j] = ld16(x + static_cast<int64_t>(c / cpr) * k + 8 * (c % cpr));
     }
     asm volatile("" ::: "memory");
 
@@ -460,10 +444,10 @@ SkinnyLdsParams lds_params(const SkinnyParams& q) {
     return p;
 }
 
-template <typename XT, typename OT, bool RES>
+template <typename OT, bool RES>
 int launch_skinny_lds(hipStream_t st, int batch, const SkinnyLdsParams& p) {
     const dim3 grid(p.cb_end[2], 1, batch), blk(64 * kSkinnyWaves);
-    hipLaunchKernelGGL((skinny_lds_kernel<XT, OT, RES>), grid, blk, 0, st, p);
+    hipLaunchKernelGGL((skinny_lds_kernel<OT, RES>), grid, blk, 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
 }
 
@@ -599,7 +583,7 @@ extern "C" int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(int dtype, s
             if (m > skinny_max_m()) {  // k == 0 with many rows: the product is zero
                 if (hipMemsetAsync(out, 0, batch_elems * m * n * 2, nullptr) != hipSuccess) return 270;
             } else if (k > 0 && lds_path(dev, m, k, batch, p.cb_end[2])) {
-                if (launch_skinny_lds<bf16_t, bf16_t, false>(nullptr, batch, lds_params(p)) != 0) return 270;
+                if (launch_skinny_lds<bf16_t, false>(nullptr, batch, lds_params(p)) != 0) return 270;
             } else if (launch_skinny<bf16_t, false>(dev, nullptr, batch, p) != 0) {
                 return 270;  // the reference's launch-failure code covers a workspace failure too
             }
@@ -662,8 +646,8 @@ extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, voi
         p.k = k;
         int rc;
         if (k > 0 && lds_path(dev, m, k, 1, p.cb_end[2]))
-            rc = f32 ? launch_skinny_lds<bf16_t, float, true>(st, 1, lds_params(p))
-                     : launch_skinny_lds<bf16_t, bf16_t, true>(st, 1, lds_params(p));
+            rc = f32 ? launch_skinny_lds<float, true>(st, 1, lds_params(p))
+                     : launch_skinny_lds<bf16_t, true>(st, 1, lds_params(p));
         else
             rc = f32 ? launch_skinny<float, true>(dev, st, 1, p) : launch_skinny<bf16_t, true>(dev, st, 1, p);
         if (rc) return rc;
@@ -744,7 +728,7 @@ extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stre
         p.k = k;
         if (p.cb_end[2] > 0) {
             const int rc = lds_path(dev, m, k, 1, p.cb_end[2])
-                               ? launch_skinny_lds<bf16_t, bf16_t, false>(st, 1, lds_params(p))
+                               ? launch_skinny_lds<bf16_t, false>(st, 1, lds_params(p))
                                : launch_skinny<bf16_t, false>(dev, st, 1, p);
             if (rc) return rc;
         }
