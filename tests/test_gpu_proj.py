@@ -50,6 +50,7 @@ def test_matmul_known_answer():
 @pytest.mark.parametrize("batch,m,n,k", [
     (1, 1, 64, 4096), (1, 8, 4096, 4096), (1, 17, 100, 264), (2, 16, 40, 72), (1, 64, 48, 512),
     (1, 65, 128, 256), (1, 300, 96, 200), (1, 5, 33, 100), (2, 130, 64, 96),
+    (2, 8, 4096, 1024), (3, 16, 2048, 2048),  # the LDS-staged kernel with a batch dimension
 ])
 def test_matmul_matches_oracle(batch, m, n, k):
     announce(f"matmul batch={batch} m={m} n={n} k={k}")
