@@ -155,6 +155,12 @@ __device__ __forceinline__ float load_agent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Workgroup barrier that waits only for LDS traffic: unlike __syncthreads it
+// leaves outstanding global loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 }  // namespace ssa
 
 // ----------------------------------------------------------------------------

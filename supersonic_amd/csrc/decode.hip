@@ -291,6 +291,72 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     const bool owner = p.fused && pos >= t_begin && pos < t_end;
     SSA_DSTAMP(0);
 
+    const int n_s = lane & 15;           // score lane: token within the block
+    const int vt = lane / LPT;           // V lane: token within the instruction
+    const int vd = (lane % LPT) * 8;     // V lane: first dim
+    // Cached tokens of this split; the owner's new token (the last one) is
+    // handled after the loop.
+    const int t_main = owner ? pos : t_end;
+    const int nblk = (t_main - t_begin + 15) >> 4;
+    const uint8_t* kbase = p.kv.k;
+    const uint8_t* vbase = p.kv.v;
+
+    // Block data of one 16-token block, loaded one block ahead (registers).
+    struct Blk {
+        op_t kb[FP8 ? 1 : KSTEPS];
+        u32x4_v kr8[FP8 ? KSTEPS / 2 : 1];  // raw e4m3 K, 16 dims a load: converted when the block is processed
+        u32x4_v vr16[FP8 ? 1 : VINS];
+        u32x2_v vr8[FP8 ? VINS : 1];
+        float ksc, vsc;
+    };
+    // Buffer resources bound to the block's live rows (a block lies inside one
+    // page): rows past kv_len read as zeros, so every load is one per-lane
+    // offset plus a constant, with no per-load clamping.
+    const int k_lane_off = n_s * D * ESZ + kdim<FP8>(0, lane >> 4) * ESZ;
+    // Cache policy of the K/V loads: nontemporal for the bf16 8-wave kernel
+    // (every byte is read once; 6.0 -> 7.1 TB/s for its access pattern on
+    // MI355X); the FP8 and 4-wave variants measured faster without it.
+    constexpr int kStream = (!FP8 && NW == 8) ? 2 : 0;
+    const int v_lane_off = (vt * D + vd) * ESZ;
+    auto fetch = [&](int blk, Blk& B) {
+        const int t0 = t_begin + blk * 16;
+        // The page comes through the scalar cache (lgkmcnt): waiting for it
+        // does not wait for the other block's vector loads still in flight.
+        const int ub = __builtin_amdgcn_readfirstlane(b), uk = __builtin_amdgcn_readfirstlane(kvh);
+        const int ut = __builtin_amdgcn_readfirstlane(t0);
+        const int64_t base = p.kv.row_uniform(ub, uk, ut, D);
+        const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(16, t_main - t0)));  // wave-uniform
+        const __amdgpu_buffer_rsrc_t kr = uniform_rsrc(kbase + base * ESZ, nvalid * D * ESZ);
+        const __amdgpu_buffer_rsrc_t vr = uniform_rsrc(vbase + base * ESZ, nvalid * D * ESZ);
+        // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
+        if constexpr (!FP8) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+                B.kb[s] = as_op<op_t>(__builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * s, 0, kStream)));
+        } else {
+            // raw bytes only, 16 per lane: converted when the block is processed
+#pragma unroll
+            for (int ss = 0; ss < KSTEPS / 2; ++ss)
+                B.kr8[ss] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * ss, 0, kStream));
+        }
+        // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
+#pragma unroll
+        for (int j = 0; j < VINS; ++j) {
+            const int jo = TPI * j * D * ESZ;
+            if constexpr (!FP8) B.vr16[j] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane_off, jo, kStream));
+            else B.vr8[j] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane_off, jo, kStream));
+        }
+        B.ksc = 1.f;
+        B.vsc = 1.f;
+        if constexpr (FP8) {
+            const int64_t sb = p.kv.srow_uniform(ub, uk, ut);
+            const int kn = min(n_s, nvalid - 1);
+            B.ksc = p.kv.ks[sb + kn];
+            B.vsc = p.kv.vs[sb + kn];
+        }
+    };
+
+    Blk A, Bn;  // the block register sets (A's first fetch is issued in the prologue)
     // ---------------------------------------------------------------- prologue
     if (tid == 0) next_blk = NW;  // blocks 0 .. NW-1 are the waves' first
     // One wave per row: rows 0 .. G-1 are the q heads, row G (owner split of
@@ -301,27 +367,48 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         constexpr int EPL = D / 64;
         const int hr = p.fused ? p.half_rot : 0;
         const int rows = G + (owner ? 1 : 0);
-        for (int r = wave; r < rows; r += NW) {
+        // A row's global loads (q head, or the new k with v), clamped to a real
+        // row so they need no branch.
+        auto row_loads = [&](const int r, float (&x)[EPL], float (&vx)[EPL], float (&w)[EPL], float (&cs)[EPL],
+                             float (&sn)[EPL]) {
+            // Branch-free: every pointer is chosen per wave (an absent input is
+            // replaced by the row itself, a valid address whose value is then
+            // ignored) and every index is clamped, so the row's loads go out
+            // back to back and one wait covers them all.
             const bool is_k = r == G;
-            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
+            const uint16_t* qrow = reinterpret_cast<const uint16_t*>(p.q) + b * p.q_bstride +
+                                   static_cast<int64_t>(kvh * G + min(r, G - 1)) * p.q_hstride;
+            const int64_t ko = (static_cast<int64_t>(b) * p.Hkv + kvh) * D;
+            const uint16_t* xsrc = is_k ? p.k_new + ko : qrow;
+            const uint16_t* vsrc = is_k ? p.v_new + ko : qrow;
+            const uint16_t* wsrc = p.fused ? (is_k ? p.k_norm_w : p.q_norm_w) : qrow;
+            const uint16_t* ctab = hr > 0 ? p.cos_t + static_cast<int64_t>(pos) * hr : qrow;
+            const uint16_t* stab = hr > 0 ? p.sin_t + static_cast<int64_t>(pos) * hr : qrow;
+            uint32_t xr[EPL], vr[EPL], wr[EPL], cr[EPL], sr[EPL];
 #pragma unroll
             for (int k = 0; k < EPL; ++k) {
                 const int d = lane + 64 * k;
-                if (!is_k) {
-                    x[k] = Elem<QT>::to_f32(p.q[b * p.q_bstride + (kvh * G + r) * p.q_hstride + d]);
-                } else {
-                    const int64_t o = (static_cast<int64_t>(b) * p.Hkv + kvh) * D + d;
-                    x[k] = bf16_bits_to_f32(p.k_new[o]);
-                    vx[k] = bf16_bits_to_f32(p.v_new[o]);
-                }
-                if (p.fused) w[k] = bf16_bits_to_f32((is_k ? p.k_norm_w : p.q_norm_w)[d]);
-                cs[k] = sn[k] = 0.f;
-                if (d < 2 * hr) {
-                    const int64_t ti = static_cast<int64_t>(pos) * hr + (d < hr ? d : d - hr);
-                    cs[k] = bf16_bits_to_f32(p.cos_t[ti]);
-                    sn[k] = bf16_bits_to_f32(p.sin_t[ti]);
-                }
+                const int ti = d < hr ? d : (d < 2 * hr ? d - hr : 0);
+                xr[k] = xsrc[d];
+                vr[k] = vsrc[d];
+                wr[k] = wsrc[d];
+                cr[k] = ctab[ti];
+                sr[k] = stab[ti];
             }
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                const int d = lane + 64 * k;
+                x[k] = is_k ? bf16_bits_to_f32(xr[k]) : Elem<QT>::to_f32(xr[k]);
+                vx[k] = bf16_bits_to_f32(vr[k]);
+                w[k] = bf16_bits_to_f32(wr[k]);
+                const bool rot = d < 2 * hr;
+                cs[k] = rot ? bf16_bits_to_f32(cr[k]) : 0.f;
+                sn[k] = rot ? bf16_bits_to_f32(sr[k]) : 0.f;
+            }
+        };
+        auto row_compute = [&](const int r, float (&x)[EPL], float (&vx)[EPL], float (&w)[EPL], float (&cs)[EPL],
+                               float (&sn)[EPL]) {
+            const bool is_k = r == G;
             float* row = is_k ? kn_s : &smem[r * D];
             if (p.fused) {
                 // Per-head RMSNorm with (1 + w), bf16 result (full_attention_4b.hip:5142-5191).
@@ -359,14 +446,32 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
                 row[lane + 64 * k] = x[k];
                 if (is_k) vn_s[lane + 64 * k] = vx[k];
             }
+        };
+        // This wave's first row goes out first, then the wave's first K/V
+        // block: waiting for the row (vmcnt drains in issue order) does not
+        // wait for the block, whose round trip overlaps the norm and RoPE.
+        {
+            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
+            row_loads(min(wave, rows - 1), x, vx, w, cs, sn);
+            fetch(max(0, min(wave, nblk - 1)), A);
+            if (wave < rows) row_compute(wave, x, vx, w, cs, sn);
+        }
+        for (int r = wave + NW; r < rows; r += NW) {
+            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
+            row_loads(r, x, vx, w, cs, sn);
+            row_compute(r, x, vx, w, cs, sn);
         }
         // heads G .. GP-1 are zero rows of the padded MFMA operand
         for (int idx = G * D + tid; idx < GP * D; idx += NT) smem[idx] = 0.f;
     }
-    __syncthreads();
+    lds_barrier();
     if (p.fused && owner) {
         // KV append at slot pos (:5226-5296); FP8 uses the absmax scale and OCP e4m3.
-        const int64_t off = p.kv.row(b, kvh, pos, D);
+        // uniform indices: the table entry comes through the scalar cache and
+        // the wait for it leaves the first K/V block's loads in flight
+        const int ub = __builtin_amdgcn_readfirstlane(b), uk = __builtin_amdgcn_readfirstlane(kvh);
+        const int up = __builtin_amdgcn_readfirstlane(pos);
+        const int64_t off = p.kv.row_uniform(ub, uk, up, D);
         if constexpr (!FP8) {
             uint16_t* kc = reinterpret_cast<uint16_t*>(p.kv.k) + off;
             uint16_t* vc = reinterpret_cast<uint16_t*>(p.kv.v) + off;
@@ -388,7 +493,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
                                                        src[d + 2] * inv, src[d + 3] * inv);
                     *reinterpret_cast<uint32_t*>(dst + d) = c4;
                 }
-                if (lane == 0) (wave == 0 ? p.kv.ks : p.kv.vs)[p.kv.srow(b, kvh, pos)] = sc;
+                if (lane == 0) (wave == 0 ? p.kv.ks : p.kv.vs)[p.kv.srow_uniform(ub, uk, up)] = sc;
             }
         }
     }
@@ -405,17 +510,17 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
             const int dk = kdim<FP8>(s, lane >> 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float a = 0.f, c = 0.f;
-                if (hh < G) {
-                    a = smem[hh * D + dk + 2 * j];
-                    c = smem[hh * D + dk + 2 * j + 1];
-                }
-                w[j] = pack2<QT>(a, c);
+                // clamped read and a select: a branch here would make the
+                // compiler wait for the wave's outstanding K/V loads
+                const int hc = min(hh, G - 1);
+                const float a = smem[hc * D + dk + 2 * j];
+                const float c = smem[hc * D + dk + 2 * j + 1];
+                w[j] = hh < G ? pack2<QT>(a, c) : 0u;
             }
             qop_s[s * 64 + lane] = w;
         }
     }
-    __syncthreads();  // smem is reused by the merge below
+    lds_barrier();  // smem is reused by the merge below
 
     // ---------------------------------------------------------------- main loop
     SSA_DSTAMP(1);
@@ -427,71 +532,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     for (int h = 0; h < GP; ++h)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-
-    const int n_s = lane & 15;           // score lane: token within the block
-    const int vt = lane / LPT;           // V lane: token within the instruction
-    const int vd = (lane % LPT) * 8;     // V lane: first dim
-    // Cached tokens of this split; the owner's new token (the last one) is
-    // handled after the loop.
-    const int t_main = owner ? pos : t_end;
-    const int nblk = (t_main - t_begin + 15) >> 4;
-    const uint8_t* kbase = p.kv.k;
-    const uint8_t* vbase = p.kv.v;
-
-    // Block data of one 16-token block, loaded one block ahead (registers).
-    struct Blk {
-        op_t kb[FP8 ? 1 : KSTEPS];
-        u32x4_v kr8[FP8 ? KSTEPS / 2 : 1];  // raw e4m3 K, 16 dims a load: converted when the block is processed
-        u32x4_v vr16[FP8 ? 1 : VINS];
-        u32x2_v vr8[FP8 ? VINS : 1];
-        float ksc, vsc;
-    };
-    // Buffer resources bound to the block's live rows (a block lies inside one
-    // page): rows past kv_len read as zeros, so every load is one per-lane
-    // offset plus a constant, with no per-load clamping.
-    const int k_lane_off = n_s * D * ESZ + kdim<FP8>(0, lane >> 4) * ESZ;
-    // Cache policy of the K/V loads: nontemporal for the bf16 8-wave kernel
-    // (every byte is read once; 6.0 -> 7.1 TB/s for its access pattern on
-    // MI355X); the FP8 and 4-wave variants measured faster without it.
-    constexpr int kStream = (!FP8 && NW == 8) ? 2 : 0;
-    const int v_lane_off = (vt * D + vd) * ESZ;
-    auto fetch = [&](int blk, Blk& B) {
-        const int t0 = t_begin + blk * 16;
-        // The page comes through the scalar cache (lgkmcnt): waiting for it
-        // does not wait for the other block's vector loads still in flight.
-        const int ub = __builtin_amdgcn_readfirstlane(b), uk = __builtin_amdgcn_readfirstlane(kvh);
-        const int ut = __builtin_amdgcn_readfirstlane(t0);
-        const int64_t base = p.kv.row_uniform(ub, uk, ut, D);
-        const int nvalid = min(16, t_main - t0);
-        const __amdgpu_buffer_rsrc_t kr = uniform_rsrc(kbase + base * ESZ, nvalid * D * ESZ);
-        const __amdgpu_buffer_rsrc_t vr = uniform_rsrc(vbase + base * ESZ, nvalid * D * ESZ);
-        // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
-        if constexpr (!FP8) {
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s)
-                B.kb[s] = as_op<op_t>(__builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * s, 0, kStream)));
-        } else {
-            // raw bytes only, 16 per lane: converted when the block is processed
-#pragma unroll
-            for (int ss = 0; ss < KSTEPS / 2; ++ss)
-                B.kr8[ss] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * ss, 0, kStream));
-        }
-        // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
-#pragma unroll
-        for (int j = 0; j < VINS; ++j) {
-            const int jo = TPI * j * D * ESZ;
-            if constexpr (!FP8) B.vr16[j] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane_off, jo, kStream));
-            else B.vr8[j] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane_off, jo, kStream));
-        }
-        B.ksc = 1.f;
-        B.vsc = 1.f;
-        if constexpr (FP8) {
-            const int64_t sb = p.kv.srow_uniform(ub, uk, ut);
-            const int kn = min(n_s, nvalid - 1);
-            B.ksc = p.kv.ks[sb + kn];
-            B.vsc = p.kv.vs[sb + kn];
-        }
-    };
 
     // One 16-token block: scores on the MFMA pipe, online softmax per head,
     // PV on VALU.  Tokens n_s >= nv are masked.  vdec(j, vf) yields the 8
@@ -607,10 +647,8 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         return __builtin_amdgcn_readfirstlane(v);
     };
     {
-        Blk A, Bn;
         int c0 = wave, c1 = nblk;
         if (c0 < nblk) {
-            fetch(c0, A);
             c1 = take();
             if (c1 < nblk) fetch(c1, Bn);
         }

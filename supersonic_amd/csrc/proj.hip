@@ -276,10 +276,6 @@ struct SkinnyLdsParams {
     int64_t x_bs, w_bs, o_bs;
 };
 
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 template <typename OT, bool RES>
 __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_eu(4))) void skinny_lds_kernel(SkinnyLdsParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[kXsMax + 16 * 8];
