@@ -350,7 +350,7 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         B.vsc = 1.f;
         if constexpr (FP8) {
             const int64_t sb = p.kv.srow_uniform(ub, uk, ut);
-            const int kn = min(n_s, nvalid - 1);
+            const int kn = max(0, min(n_s, nvalid - 1));  // nvalid is 0 when a split holds only the new token
             B.ksc = p.kv.ks[sb + kn];
             B.vsc = p.kv.vs[sb + kn];
         }
