@@ -140,6 +140,7 @@ def test_fused_decode_golden():
     (2, 16, 4, 256, 64, [300, 15]),
     (3, 8, 1, 128, 32, [1, 64, 129]),
     (1, 4, 2, 64, 16, [0]),                      # first token: attention over itself
+    (1, 16, 4, 256, 64, [256]),                  # 128-token chunks: the owner split holds only the new token
 ])
 def test_fused_decode_bf16(B, Hq, Hkv, D, rot, lens):
     announce(f"fused decode bf16 B={B} Hq={Hq} Hkv={Hkv} D={D} lens={lens}")
@@ -208,7 +209,8 @@ def test_fused_decode_caller_workspace_reuse():
         assert int(ws[:65536].count_nonzero()) == 0
 
 
-@pytest.mark.parametrize("B,lens", [(4, [1024, 16383, 5000, 77]), (2, [0, 33])])
+# [256]: chunks of 128 tokens, so the owner split holds only the new token
+@pytest.mark.parametrize("B,lens", [(4, [1024, 16383, 5000, 77]), (2, [0, 33]), (1, [256])])
 def test_fused_decode_fp8(B, lens):
     announce(f"fused decode fp8 lens={lens}")
     case = make_decode_case(31, B, 16, 4, 256, 64, lens, fp8=True)
