@@ -113,8 +113,6 @@ class Workloads:
     def __init__(self, torch, K, dev, steps, warmup):
         self.torch, self.K, self.dev = torch, K, dev
         self.steps, self.warmup = steps, warmup
-        from oracle import attn_oracle  # only for rope tables of the synthetic inputs
-        self.O = attn_oracle
 
     # ------------------------------------------------------------ helpers
     def randn(self, *shape, dtype=None, seed=0):
@@ -167,7 +165,7 @@ class Workloads:
         v_new = self.randn(B, Hkv * D, seed=seed + 2)
         qw = (self.randn(D, seed=seed + 3).float() * 0.02 + 1).bfloat16()
         kw = (self.randn(D, seed=seed + 4).float() * 0.02 + 1).bfloat16()
-        cos, sin = self.O.rope_tables(rot, cap + 1, 1.0e7)
+        cos, sin = K.rope_tables(rot, cap + 1, 1.0e7)
         pos = torch.tensor(lens, dtype=torch.int32, device=self.dev)
         per_cache = B * Hkv * cap * D * (1 if fp8 else 2) * 2
         n_copies = max(1, min(8, math.ceil(2 * MALL_BYTES / per_cache)))
@@ -250,7 +248,7 @@ class Workloads:
         v_new = self.randn(S, Hkv * D, seed=seed + 2)
         qw = (self.randn(D, seed=seed + 3).float() * 0.02 + 1).bfloat16()
         kw = (self.randn(D, seed=seed + 4).float() * 0.02 + 1).bfloat16()
-        cos, sin = self.O.rope_tables(rot, start + S + 1, 1.0e7)
+        cos, sin = K.rope_tables(rot, start + S + 1, 1.0e7)
         cos, sin = cos.to(self.dev), sin.to(self.dev)
         L = start + S
         if paged_ps:
@@ -374,7 +372,7 @@ class Workloads:
         o_proj + residual) per step, eager launches against a HIP graph replay of
         the same launches: config 1 heads (B=1, 8/2 heads, 2048 cached tokens,
         hidden 1024) and config 2 (B=8, 16/4 heads, 32768 cached, hidden 4096)."""
-        torch, K, O = self.torch, self.K, self.O
+        torch, K = self.torch, self.K
         res = {}
         for name, (B, Hq, Hkv, hid, L) in {"config1": (1, 8, 2, 1024, 2048),
                                            "config2_b8": (8, 16, 4, 4096, 32768)}.items():
@@ -385,8 +383,9 @@ class Workloads:
             wq, wk, wv = ((self.randn(n, hid, seed=82 + i) * hid ** -0.5).to(torch.bfloat16)
                           for i, n in enumerate((Hq * 2 * D, Hkv * D, Hkv * D)))
             wo = (self.randn(hid, Hq * D, seed=85) * (Hq * D) ** -0.5).to(torch.bfloat16)
-            qw, kw = (t.to(self.dev) for t in O.norm_weights(g, D))
-            cos, sin = (t.to(self.dev) for t in O.rope_tables(rot, L + 2, 1.0e7))
+            qw = (self.randn(D, seed=88).float() * 0.02 + 1).bfloat16()
+            kw = (self.randn(D, seed=89).float() * 0.02 + 1).bfloat16()
+            cos, sin = (t.to(self.dev) for t in K.rope_tables(rot, L + 2, 1.0e7))
             kc = self.randn(B, Hkv, L + 1, D, seed=86)
             vc = self.randn(B, Hkv, L + 1, D, seed=87)
             cache = K.KvCache(kc, vc)
@@ -442,7 +441,7 @@ class Workloads:
     def cpu_decode8(self):
         """The torch fp32 oracle on this host's cores: one config-2 B=8 step."""
         import torch
-        O = self.O
+        from oracle import attn_oracle as O  # the CPU baseline is the oracle itself
         torch.set_num_threads(min(16, os.cpu_count() or 1))
         g = torch.Generator().manual_seed(3)
         B, Hq, Hkv, D, rot, L = 8, 16, 4, 256, 64, 32768

@@ -284,6 +284,17 @@ int supersonic_attn_gfx950_quantize_kv_fp8_ocp(
  * thread; the pair is consumed by that call.  NULL, NULL clears it. */
 void supersonic_attn_gfx950_set_profile_events(void* before, void* after);
 
+/* RoPE cos / sin tables on the host, as RotaryTables::build
+ * (crates/qwen35/src/rotary.rs:15-46) builds them: inv_freq_i =
+ * theta^(-2i/rotary_dim), angle pos * inv_freq_i in double precision, each
+ * value rounded to float and then to bf16 (RNE).  cos_out / sin_out: host
+ * arrays of max_pos * rotary_dim/2 bf16 bit patterns, [max_pos, rotary_dim/2],
+ * the layout the fused entry points read (after a copy to the device).
+ * No GPU call.  Status: SUPERSONIC_ERR_ROTARY (odd rotary_dim or theta <= 0),
+ * SUPERSONIC_ERR_NULL. */
+int supersonic_attn_rope_tables(size_t rotary_dim, size_t max_pos, double theta, uint16_t* cos_out,
+                                uint16_t* sin_out);
+
 /* Library version string. */
 const char* supersonic_attn_version(void);
 

@@ -111,17 +111,22 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
     limit = torch.clamp(seqlen_offset + pos + 1, max=L)  # [S]
     mask = torch.arange(L)[None, :] < limit[:, None]     # [S, L]
     has_key = limit > 0
+    # rows are independent: blocks of query rows bound the [G, rows, L] score memory
+    rb = max(1, min(S, (1 << 27) // max(1, G * L)))
     for b in range(B):
         for hk in range(Hkv):
             kf = k[b, hk].to(F32)
             vf = v[b, hk].to(F32)
-            qf = q[b, hk * G:(hk + 1) * G].to(F32)               # [G,S,D]
-            s = torch.matmul(qf, kf.T) * scale                  # [G,S,L]
-            s = s.masked_fill(~mask, float("-inf"))
-            s = torch.where(has_key[None, :, None], s, torch.zeros_like(s))
-            p = torch.softmax(s, dim=-1)
-            p = torch.where(has_key[None, :, None], p, torch.zeros_like(p))
-            out[b, hk * G:(hk + 1) * G] = torch.matmul(p, vf)
+            for r0 in range(0, S, rb):
+                r1 = min(S, r0 + rb)
+                qf = q[b, hk * G:(hk + 1) * G, r0:r1].to(F32)         # [G,rows,D]
+                s = torch.matmul(qf, kf.T) * scale                    # [G,rows,L]
+                s = s.masked_fill(~mask[r0:r1], float("-inf"))
+                hk_rows = has_key[r0:r1][None, :, None]
+                s = torch.where(hk_rows, s, torch.zeros_like(s))
+                p = torch.softmax(s, dim=-1)
+                p = torch.where(hk_rows, p, torch.zeros_like(p))
+                out[b, hk * G:(hk + 1) * G, r0:r1] = torch.matmul(p, vf)
     return out
 
 

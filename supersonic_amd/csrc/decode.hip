@@ -147,22 +147,6 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);
 }
 
-// Optional timeline (build with -DSSA_TRACE): thread 0 of each of the first
-// 4096 workgroups stamps s_memrealtime at kernel entry, loop start, loop end,
-// after the partials, and exit; ssa_decode_trace_dump copies them out.
-#ifdef SSA_TRACE
-__device__ unsigned long long g_decode_trace[4096 * 6];
-#define SSA_DSTAMP(slot)                                                                                   \
-    do {                                                                                                   \
-        const unsigned wg_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);               \
-        if (tid == 0 && wg_ < 4096) g_decode_trace[wg_ * 6 + (slot)] = __builtin_amdgcn_s_memrealtime();   \
-    } while (0)
-#else
-#define SSA_DSTAMP(slot) \
-    do {                 \
-    } while (0)
-#endif
-
 // Waves per workgroup: 8 for head groups up to 4 (one workgroup per CU, two
 // waves per SIMD at up to 256 registers); the larger groups need more
 // registers and run 4 (two workgroups per CU for 8, one for 16).
@@ -289,7 +273,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     const int G = p.G;
     const int pos = len - 1;
     const bool owner = p.fused && pos >= t_begin && pos < t_end;
-    SSA_DSTAMP(0);
 
     const int n_s = lane & 15;           // score lane: token within the block
     const int vt = lane / LPT;           // V lane: token within the instruction
@@ -523,7 +506,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     lds_barrier();  // smem is reused by the merge below
 
     // ---------------------------------------------------------------- main loop
-    SSA_DSTAMP(1);
     float m[4], lsum[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) { m[i] = -1e30f; lsum[i] = 0.f; }
@@ -602,22 +584,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         __builtin_amdgcn_wave_barrier();
     };
     auto process_blk = [&](int blk, Blk& B) {
-#ifdef SSA_DECODE_NOCOMPUTE
-        {
-            u32x4_v x = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) {
-                if constexpr (!FP8) x ^= __builtin_bit_cast(u32x4_v, B.kb[s]);
-                else x ^= B.kr8[s >> 1];
-            }
-            if constexpr (!FP8) {
-#pragma unroll
-                for (int j = 0; j < VINS; ++j) x ^= B.vr16[j];
-            }
-            acc[0][0] += __uint_as_float(x[0] ^ x[1] ^ x[2] ^ x[3]) * 1e-30f;
-            return;
-        }
-#endif
         const int t0 = t_begin + blk * 16;
         auto vdec = [&](int j, float (&vf)[8]) {
             if constexpr (!FP8) unpack8<QT>(B.vr16[j], vf);
@@ -683,7 +649,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     }
 
     // ---------------------------------------------------------------- merge
-    SSA_DSTAMP(2);
     float ltot[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
@@ -751,7 +716,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
     }
 
     // ---------------------------------------------------------------- split merge
-    SSA_DSTAMP(3);
     // The last split of (b, kv head) to arrive merges all of them (log-sum-exp)
     // and applies the gate.  The partials are written and read with device-
     // coherent (sc1) accesses, and the writer waits for its stores to complete
@@ -766,7 +730,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         last_s = prev == static_cast<unsigned>(ns - 1);
     }
     __syncthreads();
-    SSA_DSTAMP(4);
     if (!last_s) return;
     // One online pass over the splits of each head, MCH at a time with all
     // their loads in flight together.  With at least twice as many waves as
@@ -839,7 +802,6 @@ __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(Dec
         for (int hh = wave; hh < G; hh += NW)
             merge_head(hh, 0, std::integral_constant<int, 16>{}, std::integral_constant<int, DPL>{});
     }
-    SSA_DSTAMP(5);
     if (tid == 0) p.arrivals[b * p.Hkv + kvh] = 0u;  // every split has arrived: ready for the next call
 }
 
@@ -1074,12 +1036,6 @@ static int decode_flat_common(int dtype, size_t device, size_t B, size_t Hq, siz
 }  // namespace ssa
 
 using namespace ssa;
-
-#ifdef SSA_TRACE
-extern "C" int ssa_decode_trace_dump(void* dst) {
-    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(ssa::g_decode_trace), sizeof(ssa::g_decode_trace)) == hipSuccess ? 0 : 1;
-}
-#endif
 
 extern "C" int supersonic_qwen35_hip_full_attention_decode_flat(
     int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,

@@ -150,17 +150,7 @@ __device__ __forceinline__ float xor32_sum(float x) {
 template <int D> struct Tile {
     static constexpr int ROWB = 2 * D;        // bytes per key row
     static constexpr int NR = D / 8;          // copy instructions (= 1 KB blocks) per tile
-// LDS read lookahead of the K-operand (reads) and V-operand (MFMAs) pipelines
-#ifndef SSA_KLA
-#define SSA_KLA 8
-#endif
-#ifndef SSA_VLA
-#define SSA_VLA 6
-#endif
-#ifndef SSA_KPAD
-#define SSA_KPAD 32
-#endif
-    static constexpr int KBLK = 1024 + SSA_KPAD;
+    static constexpr int KBLK = 1024 + 32;
     static constexpr int KBYTES = NR * KBLK;
     static constexpr int VBYTES = NR * 1024;
     static constexpr int STAGE = KBYTES + VBYTES;
@@ -193,46 +183,14 @@ template <> struct Mfma16<f16_t> {
     }
 };
 
+// LDS read lookahead of the K-operand (reads) and V-operand (MFMAs) pipelines
+constexpr int kKLA = 8;
+constexpr int kVLA = 6;
+
 constexpr int kPrefillWaves = 8;   // compute waves: 8 x 16 query rows = 128 rows
 constexpr int kCopyWaves = 4;      // waves that only move K / V^T tiles into LDS
 constexpr int kPrefillThreads = 64 * (kPrefillWaves + kCopyWaves);
 
-// Optional phase timeline (build with -DSSA_TRACE): wave 0 and wave 4 of the
-// first 16 workgroups stamp s_memtime at five points of each of their first
-// 64 key tiles; ssa_prefill_trace_dump copies the stamps out.
-#ifdef SSA_TRACE
-__device__ unsigned long long g_prefill_trace[16 * 2 * 64 * 6];
-#define SSA_STAMP(slot)                                                                                    \
-    do {                                                                                                   \
-        if (blockIdx.x < 16 && (wave & 3) == 0 && it < 64) {                                               \
-            __builtin_amdgcn_sched_barrier(0);                                                             \
-            const unsigned long long t_ = __builtin_amdgcn_s_memtime();                                    \
-            const unsigned long long r_ = (slot) == 0 ? __builtin_amdgcn_s_memrealtime() : 0ull;           \
-            if (lane == 0) g_prefill_trace[((blockIdx.x * 2 + (wave >> 2)) * 64 + it) * 6 + (slot)] = t_; \
-            if (lane == 0 && (slot) == 0) g_prefill_trace[((blockIdx.x * 2 + (wave >> 2)) * 64 + it) * 6 + 5] = r_; \
-            __builtin_amdgcn_sched_barrier(0);                                                             \
-        }                                                                                                  \
-    } while (0)
-// Workgroup timeline: s_memrealtime at entry (slot 0), after the query
-// prologue (1), after the key loop (2) and at exit (3), the hardware id (4),
-// the tile count (5), (XCC_ID << 32 | HW_ID in 4), after the query norm (6) and after the query RoPE (7).
-__device__ unsigned long long g_prefill_wg[4096 * 8];
-#define SSA_WG_STAMP(slot)                                                                          \
-    do {                                                                                            \
-        if (tid == 0 && (qt * p.Hq + h) * p.B + b < 4096) {                                                        \
-            g_prefill_wg[((qt * p.Hq + h) * p.B + b) * 8 + (slot)] = __builtin_amdgcn_s_memrealtime();               \
-            if ((slot) == 0) g_prefill_wg[((qt * p.Hq + h) * p.B + b) * 8 + 4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)) | (static_cast<unsigned long long>(__builtin_amdgcn_s_getreg(20 | (15 << 11))) << 32); \
-            if ((slot) == 0) g_prefill_wg[((qt * p.Hq + h) * p.B + b) * 8 + 5] = ntiles;                            \
-        }                                                                                           \
-    } while (0)
-#else
-#define SSA_WG_STAMP(slot) \
-    do {                   \
-    } while (0)
-#define SSA_STAMP(slot) \
-    do {                \
-    } while (0)
-#endif   // 8 wave64s x 16 query rows = 128 rows per workgroup
 
 // One workgroup = 128 query rows of one head: 8 compute waves of 16 rows each
 // plus 4 copy waves that only issue the global->LDS tile copies (the copy
@@ -328,7 +286,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                                                      16, (i & 1) ? vt_lane1 : vt_lane0, 8 * i * vt_rowb, 0, 0);
         }
     };
-    SSA_WG_STAMP(0);
     if constexpr (COPY) {
         // Copy waves: the next tile is issued once everyone has passed the
         // barrier of tile it (its stage's previous tile has been read) and has
@@ -409,7 +366,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                 nq[k][j] = cvt_pk<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
             st16(qs + (k * RPI + rr) * D + 8 * c, nq[k]);
         }
-        SSA_WG_STAMP(6);
         if (hr > 0) {
             // RoPE: the rotating lanes read their partner's 8 normed dims back
             // (all reads are issued before any write; LDS is in order per wave).
@@ -439,7 +395,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                 }
             }
         }
-        SSA_WG_STAMP(7);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -466,15 +421,11 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const int vx = (lane & 15) >> 1;
     const int vrd0 = T::KBYTES + 16 * (8 * (lane & 15) + (g4 ^ vx));
     const int vrd1 = T::KBYTES + 16 * (8 * (lane & 15) + ((4 + g4) ^ vx));
-
-    SSA_WG_STAMP(1);
     for (int it = 0; it < ntiles; ++it) {
         const int k0 = it * 64;
         const int st = (it + 1) & 1;
         __syncthreads();                // the copy waves' tile `it` has landed; stage st^1 is free again
-        SSA_STAMP(0);
         if (k0 >= lim_wave) continue;   // the whole tile is past this wave's rows
-        SSA_STAMP(1);
 
         const uint8_t* kl = lds + st * T::STAGE + kbase_off;
         const uint8_t* vl0 = lds + st * T::STAGE + vrd0;
@@ -492,15 +443,14 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                 sacc[kb] = Mfma16<QT>::mma(ka, qb[s], sacc[kb]);
             }
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, SSA_KLA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, kKLA, 0);
 #pragma unroll
-        for (int i = 0; i < 4 * KS - SSA_KLA; ++i) {
+        for (int i = 0; i < 4 * KS - kKLA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, SSA_KLA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kKLA, 0);
         __builtin_amdgcn_sched_barrier(0);
-        SSA_STAMP(2);
 
         // Online softmax, base 2, exact running max.  Lane holds row myrow and
         // keys k0 + 16 kb + 4 g4 + i.
@@ -553,7 +503,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
             pk[u] = to_op<op_t>(w);
         }
         __builtin_amdgcn_sched_barrier(0);
-        SSA_STAMP(3);
 
         // O^T += V^T P^T: two 32-key steps.  A operand: dims 16 d + (lane & 15),
         // the 8 keys of staging chunk 4 u + g4, which are exactly the keys
@@ -568,18 +517,16 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
             }
             lacc = Mfma16<QT>::mma(ones, pk[u], lacc);
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, SSA_VLA, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, kVLA, 1);
 #pragma unroll
-        for (int i = 0; i < 2 * DBK - SSA_VLA; ++i) {
+        for (int i = 0; i < 2 * DBK - kVLA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, SSA_VLA, 1);
-        SSA_STAMP(4);
+        __builtin_amdgcn_sched_group_barrier(0x008, kVLA, 1);
     }
 
     __syncthreads();                    // item end (the copy waves' last barrier)
-    SSA_WG_STAMP(2);
     // ------------------------------------------------ epilogue
     // O^T C layout: lane holds row myrow, dims 16 d + 4 g4 + i.
     const float l_tot = lacc[0];
@@ -619,7 +566,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
             *reinterpret_cast<u32x2_v*>(orow + dd) = o;
         }
     }
-    SSA_WG_STAMP(3);
     }  // compute waves
     };
 
@@ -988,15 +934,6 @@ static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t 
 }  // namespace ssa
 
 using namespace ssa;
-
-#ifdef SSA_TRACE
-extern "C" int ssa_prefill_wg_dump(void* dst) {
-    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(ssa::g_prefill_wg), sizeof(ssa::g_prefill_wg)) == hipSuccess ? 0 : 1;
-}
-extern "C" int ssa_prefill_trace_dump(void* dst) {
-    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(ssa::g_prefill_trace), sizeof(ssa::g_prefill_trace)) == hipSuccess ? 0 : 1;
-}
-#endif
 
 extern "C" int supersonic_qwen35_hip_full_attention_prefill(
     int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads, size_t q_len,

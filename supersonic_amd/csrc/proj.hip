@@ -264,6 +264,7 @@ __global__ __launch_bounds__(256) void input_norm_kernel(int rows, int k, float 
 // ---------------------------------------------------------------------------
 constexpr int kXsMax = 32768;  // staged elements (64 KB): two workgroups per CU
 constexpr int kXsChunks = kXsMax / 8 / 512;  // 16-byte chunks per thread at most
+constexpr int kXsDummy = kXsMax + 120;        // 16-byte slot for the chunks past the rows
 
 struct SkinnyLdsParams {
     const uint16_t* x;      // [batch][m][k] bf16
@@ -325,11 +326,14 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int j = 0; j < kSkinnySteps; ++j) wv[j] = wload(s0 + j);
 
-    // 3. stage the rows in LDS; chunks past the rows go to a dummy slot in the padding
+    // 3. stage the rows in LDS; chunks past the rows go to a dummy slot at the
+    // end of the padding.  The padded rows end at m * ldx - 8 = m * k + 8 (m - 1)
+    // <= kXsMax + 120 elements (m <= 16, m * k <= kXsMax), so the slot
+    // [kXsMax + 120, kXsMax + 128) never overlaps a row.
 #pragma unroll
     for (int j = 0; j < kXsChunks; ++j) {
         const int c = tid + 512 * j;
-        st16(c < nch ? xs + (c / cpr) * ldx + 8 * (c % cpr) : xs + kXsMax, xr[j]);
+        st16(c < nch ? xs + (c / cpr) * ldx + 8 * (c % cpr) : xs + kXsDummy, xr[j]);
     }
     lds_barrier();
 

@@ -1,8 +1,12 @@
 // Host runtime pieces shared by the bridges: the per-device workspace cache.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
 #include "common.hpp"
+#include "supersonic_attn.h"
 
 namespace ssa {
 
@@ -82,3 +86,34 @@ extern "C" void supersonic_attn_gfx950_set_profile_events(void* before, void* af
 }
 
 extern "C" const char* supersonic_attn_version(void) { return "supersonic-attn-gfx950 0.1.0"; }
+
+// RoPE tables on the host, RotaryTables::build (crates/qwen35/src/rotary.rs:15-46):
+// inv_freq_i = theta^(-2i / rotary_dim) and the angle pos * inv_freq_i in
+// double precision; each cos / sin is rounded to float, then to bf16
+// (round-to-nearest-even), the conversion chain of a double tensor cast to
+// bf16.  cos_out / sin_out are host arrays of max_pos * rotary_dim / 2 bf16
+// bit patterns, row pos holding the rotary_dim / 2 pair angles.
+static uint16_t f32_to_bf16_rne_host(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+extern "C" int supersonic_attn_rope_tables(size_t rotary_dim, size_t max_pos, double theta, uint16_t* cos_out,
+                                           uint16_t* sin_out) {
+    if (rotary_dim % 2 != 0 || !(theta > 0.0)) return SUPERSONIC_ERR_ROTARY;
+    const size_t half = rotary_dim / 2;
+    if (half == 0 || max_pos == 0) return 0;
+    if (!cos_out || !sin_out) return SUPERSONIC_ERR_NULL;
+    for (size_t i = 0; i < half; ++i) {
+        const double freq = 1.0 / std::pow(theta, 2.0 * static_cast<double>(i) / static_cast<double>(rotary_dim));
+        for (size_t p = 0; p < max_pos; ++p) {
+            const double ang = static_cast<double>(p) * freq;
+            cos_out[p * half + i] = f32_to_bf16_rne_host(static_cast<float>(std::cos(ang)));
+            sin_out[p * half + i] = f32_to_bf16_rne_host(static_cast<float>(std::sin(ang)));
+        }
+    }
+    return 0;
+}

@@ -96,6 +96,7 @@ SIGNATURES = {
     "supersonic_attn_gfx950_qkv_proj": [_sz, _p, _i, _sz, _sz, _sz, _sz, _f, _p, _p, _p, _p, _p, _p, _p, _p],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "supersonic_attn_gfx950_set_profile_events": [_p, _p],
+    "supersonic_attn_rope_tables": [_sz, _sz, C.c_double, _p, _p],
     "supersonic_attn_version": [],
 }
 RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
@@ -368,6 +369,18 @@ def set_profile_events(before, after):
     """Arm the benchmark hook with two torch.cuda.Event (enable_timing=True)."""
     load().supersonic_attn_gfx950_set_profile_events(None if before is None else before.cuda_event,
                                                      None if after is None else after.cuda_event)
+
+
+def rope_tables(rotary_dim, max_pos, theta):
+    """``supersonic_attn_rope_tables``: host (CPU) bf16 tensors ``(cos, sin)`` of
+    shape ``[max_pos, rotary_dim // 2]``, built by the library."""
+    import torch
+    half = rotary_dim // 2
+    cos = torch.empty(max_pos, half, dtype=torch.bfloat16)
+    sin = torch.empty(max_pos, half, dtype=torch.bfloat16)
+    _check("rope_tables", load().supersonic_attn_rope_tables(rotary_dim, max_pos, float(theta), _ptr(cos),
+                                                             _ptr(sin)))
+    return cos, sin
 
 
 def version() -> str:

@@ -20,6 +20,18 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(names) == set(K.SIGNATURES)
 
 
+def test_library_exports_exactly_the_header():
+    """The shipped .so exports the header's functions and nothing else of its
+    own (no probe or trace entry points)."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm") or "/usr/bin/nm"
+    out = subprocess.run([nm, "-D", "--defined-only", K.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    funcs = {ln.split()[-1] for ln in out.splitlines() if len(ln.split()) == 3 and ln.split()[1] == "T"}
+    ours = {f for f in funcs if f.startswith(("supersonic_", "ssa_"))}
+    assert ours == set(K.header_functions())
+
+
 def test_reference_symbols_are_declared():
     """The drop-in set: every reference bridge symbol on the path
     (prefill_ffi.rs:635-950) is declared with the reference's name."""
@@ -119,3 +131,21 @@ def test_workspace_size_is_host_only(lib):
     n = K.decode_workspace_size(1, 16, 4, 256, 32769)
     assert n > 16 * 256 * 4
     assert K.decode_workspace_size(8, 16, 4, 256, 32769) >= n
+
+
+@pytest.mark.parametrize("rot,max_pos,theta", [(64, 70000, 1.0e7), (32, 4097, 1.0e4), (128, 513, 1.0e6)])
+def test_rope_tables_match_oracle(lib, rot, max_pos, theta):
+    """The library's host table builder equals the oracle's RotaryTables::build
+    restatement (itself pinned by a float64 brute force) bit for bit."""
+    from oracle import attn_oracle as O
+    import torch
+    cos, sin = K.rope_tables(rot, max_pos, theta)
+    rc, rs = O.rope_tables(rot, max_pos, theta)
+    assert torch.equal(cos.view(torch.int16), rc.view(torch.int16))
+    assert torch.equal(sin.view(torch.int16), rs.view(torch.int16))
+
+
+def test_rope_tables_validation(lib):
+    assert lib.supersonic_attn_rope_tables(63, 4, 1e4, None, None) == K.ERR["ROTARY"]
+    assert lib.supersonic_attn_rope_tables(64, 4, 0.0, None, None) == K.ERR["ROTARY"]
+    assert lib.supersonic_attn_rope_tables(64, 4, 1e4, None, None) == K.ERR["NULL"]

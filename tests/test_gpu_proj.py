@@ -62,6 +62,21 @@ def test_matmul_matches_oracle(batch, m, n, k):
     assert_ulps(out, ref, ulp(ref) + 1e-6, "matmul")
 
 
+@pytest.mark.parametrize("m,k", [(12, 2728), (15, 2184), (16, 2048)])
+def test_matmul_lds_staging_padded_rows(m, k, monkeypatch):
+    """The LDS-staged kernel with rows whose padded end, m * k + 8 (m - 1), passes
+    32768 elements: the surplus 16-byte chunks of the staging loop must not land
+    inside a row."""
+    announce(f"matmul lds staging m={m} k={k}")
+    monkeypatch.setenv("SUPERSONIC_PROJ_SKINNY_MAX_M", "16")
+    g = gen(84)
+    lhs = O.randn_bf16(g, 1, m, k)
+    rhs = O.randn_bf16(g, 1, 4096, k, std=k ** -0.5)
+    out = dropin_matmul(lhs, rhs)
+    ref = O.matmul_rhs_transposed(lhs, rhs)
+    assert_ulps(out, ref, ulp(ref) + 1e-6, "matmul lds staging")
+
+
 def test_matmul_empty_k_gives_zeros():
     out = torch.full((1, 3, 5), 7.0, dtype=torch.bfloat16, device=DEV)
     K.matmul_rhs_transposed(0, K.ScalarType.BF16, 1, 3, 5, 0, torch.zeros(8, device=DEV),
