@@ -218,18 +218,31 @@ int supersonic_attn_gfx950_decode_attend(
     float scale, const void* q, const int32_t* kv_lens, const supersonic_kv_cache* cache,
     const void* gate, void* out, void* workspace, size_t workspace_bytes);
 
+/* Bytes of workspace supersonic_attn_gfx950_prefill needs for a chunk of
+ * chunk_len tokens starting at chunk_start (the staged V^T rows of every
+ * position, and for an fp8 cache the bf16 K rows the attention reads).  No
+ * GPU call. */
+size_t supersonic_attn_gfx950_prefill_workspace_size(
+    int kv_dtype, size_t kv_heads, size_t head_dim, size_t chunk_len, size_t chunk_start);
+
 /* One prefill chunk of one sequence (cache sequence index 0): tokens at
  * positions chunk_start .. chunk_start+chunk_len-1.  Q/K RMSNorm + RoPE, K/V
  * written to the cache (bf16, or fp8 with scales), causal MFMA attention over
  * the cached prefix plus the chunk, sigmoid gate.  q_proj [S, Hq*2D],
- * k_new/v_new [S, Hkv*D], out [S, Hq*D], all bf16.  Asynchronous on `stream`. */
+ * k_new/v_new [S, Hkv*D], out [S, Hq*D], all bf16.  Asynchronous on `stream`.
+ * workspace: caller device memory of at least
+ * supersonic_attn_gfx950_prefill_workspace_size() bytes (no allocation, no
+ * synchronisation: the call can be captured into a HIP graph; calls sharing a
+ * workspace must not overlap), or NULL for a library-owned buffer per device
+ * (grown on demand with a device synchronisation; overlapping calls on one
+ * device then race). */
 int supersonic_attn_gfx950_prefill(
     size_t device_ordinal, void* stream, int kv_dtype,
     size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
     size_t chunk_len, size_t chunk_start, float eps, float scale,
     const void* q_proj, const void* k_new, const void* v_new,
     const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
-    const supersonic_kv_cache* cache, void* out);
+    const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes);
 
 /* Input RMSNorm + Q/K/V projections, before the attention:
  *   normed = bf16(hidden * rsqrt(mean(hidden^2) + eps) * (1 + input_norm_w))
@@ -242,17 +255,22 @@ int supersonic_attn_gfx950_prefill(
  * supersonic_attn_gfx950_decode (q_out_dim = q_heads * 2 * head_dim).  Replaces
  * the megakernel's input norm and projections (full_attention_4b.hip:4942-4967,
  * :5019-5101) and rms_norm_rows_model + matmul_proj of prefill_engine.rs:1951-2117.
- * A norm kernel writes the normed rows once (library workspace), then rows <= 12
+ * A norm kernel writes the normed rows once (workspace), then rows <= 12
  * (SUPERSONIC_PROJ_SKINNY_MAX_M) with q/kv_out_dim % 16 == 0 take one
  * weight-streaming launch over the three matrices; otherwise one hipBLASLt GEMM
- * per matrix.  hidden_dim % 8 == 0.  Asynchronous on `stream`.  The normed rows
- * live in a library workspace per device: calls that overlap on one device
- * (different streams) race. */
+ * per matrix.  hidden_dim % 8 == 0.  Asynchronous on `stream`.  workspace:
+ * caller device memory of at least supersonic_attn_gfx950_qkv_proj_workspace_size()
+ * bytes, zero-filled before its first use and not written by the caller
+ * between calls (split-k arrival counters that every call leaves at zero);
+ * calls sharing it must not overlap.  NULL: library-owned buffers per device
+ * (grown on demand; overlapping calls on one device then race). */
+size_t supersonic_attn_gfx950_qkv_proj_workspace_size(
+    size_t rows, size_t hidden_dim, size_t q_out_dim, size_t kv_out_dim);
 int supersonic_attn_gfx950_qkv_proj(
     size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim,
     size_t q_out_dim, size_t kv_out_dim, float eps, const void* hidden, const void* input_norm_w,
     const void* q_proj_w, const void* k_proj_w, const void* v_proj_w, void* q_proj_out,
-    void* k_out, void* v_out);
+    void* k_out, void* v_out, void* workspace, size_t workspace_bytes);
 
 /* Output projection with the residual add, after the gated attention:
  *   hidden[r, j] = bf16(hidden[r, j] + bf16(sum_c attn[r, c] * o_proj_w[j, c]))
@@ -263,12 +281,16 @@ int supersonic_attn_gfx950_qkv_proj(
  * step G (full_attention_4b.hip:5481-5577) and matmul_proj + residual_add of
  * prefill_engine.rs:2308-2334.  rows <= 12 (SUPERSONIC_PROJ_SKINNY_MAX_M, at most 64) with attn_dim % 8 == 0: one
  * HBM-streaming MFMA kernel with the residual fused; otherwise hipBLASLt and a
- * residual kernel.  Asynchronous on `stream`.  Split-k partials, arrival
- * counters and the GEMM output live in library workspaces per device: calls
- * that overlap on one device (different streams) race. */
+ * residual kernel.  Asynchronous on `stream`.  workspace: split-k partials
+ * and arrival counters, or the GEMM output rows; caller device memory of at
+ * least supersonic_attn_gfx950_o_proj_workspace_size() bytes under the same
+ * rules as supersonic_attn_gfx950_qkv_proj's, or NULL for library-owned
+ * buffers per device. */
+size_t supersonic_attn_gfx950_o_proj_workspace_size(size_t rows, size_t hidden_dim, size_t attn_dim);
 int supersonic_attn_gfx950_o_proj_residual(
     size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim,
-    size_t attn_dim, const void* attn, const void* o_proj_w, void* hidden);
+    size_t attn_dim, const void* attn, const void* o_proj_w, void* hidden,
+    void* workspace, size_t workspace_bytes);
 
 /* OCP e4m3 variant of supersonic_qwen35_4b_hip_quantize_kv_to_fp8: same
  * layout and scale rule (scale = max(absmax/448, 1e-12)), hardware OCP

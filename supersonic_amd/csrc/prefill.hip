@@ -951,11 +951,20 @@ extern "C" int supersonic_qwen35_4b_hip_full_attention_prefill(
                           num_kv_groups, scale, seqlen_offset, query, key, value, out);
 }
 
+extern "C" size_t supersonic_attn_gfx950_prefill_workspace_size(int kv_dtype, size_t kv_heads, size_t head_dim,
+                                                                size_t chunk_len, size_t chunk_start) {
+    const size_t L = chunk_start + chunk_len;
+    if (L > 0x7FFFFFFF || kv_heads > 4096 || head_dim > 512) return 0;
+    const size_t ld = (L + 63) / 64 * 64;
+    const size_t stage = kv_heads * head_dim * ld * 2;  // V^T staging
+    return kv_dtype == SUPERSONIC_KV_FP8_E4M3 ? 2 * stage : stage;  // + the bf16 K rows of an fp8 cache
+}
+
 extern "C" int supersonic_attn_gfx950_prefill(
     size_t device_ordinal, void* stream, int kv_dtype, size_t q_heads, size_t kv_heads, size_t head_dim,
     size_t rotary_dim, size_t chunk_len, size_t chunk_start, float eps, float scale, const void* q_proj,
     const void* k_new, const void* v_new, const void* q_norm_w, const void* k_norm_w, const void* cos_table,
-    const void* sin_table, const supersonic_kv_cache* cache, void* out) {
+    const void* sin_table, const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes) {
     if (kv_dtype != SUPERSONIC_KV_BF16 && kv_dtype != SUPERSONIC_KV_FP8_E4M3) return SUPERSONIC_ERR_DTYPE;
     const bool fp8 = kv_dtype == SUPERSONIC_KV_FP8_E4M3;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return SUPERSONIC_ERR_HEAD_DIM;
@@ -1001,8 +1010,13 @@ extern "C" int supersonic_attn_gfx950_prefill(
         const int ld = (p.L + 63) / 64 * 64;
         // V^T staging, then (fp8 cache) the bf16 K rows the attention reads
         const size_t stage_bytes = static_cast<size_t>(p.Hkv) * head_dim * ld * 2;
-        void* ws = device_workspace(static_cast<int>(device_ordinal), fp8 ? 2 * stage_bytes : stage_bytes,
-                                    kWorkspacePrefill);
+        const size_t need = fp8 ? 2 * stage_bytes : stage_bytes;
+        void* ws = workspace;
+        if (ws) {
+            if (workspace_bytes < need) return SUPERSONIC_ERR_WORKSPACE;
+        } else {
+            ws = device_workspace(static_cast<int>(device_ordinal), need, kWorkspacePrefill);
+        }
         if (!ws) return SUPERSONIC_ERR_WORKSPACE;
         p.vt = static_cast<const uint16_t*>(ws);
         p.vt_ld = ld;

@@ -371,6 +371,14 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_
     }
 }
 
+// Zero fill (a kernel rather than hipMemsetAsync, so the call can be captured
+// into a HIP graph without a memset node).
+__global__ void fill_u16_kernel(size_t total, uint16_t* y) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        y[i] = 0;
+}
+
 // hidden = bf16(hidden + y) over `total` elements (y bf16).
 template <typename OT>
 __global__ void residual_add_kernel(size_t total, const uint16_t* y, OT* hidden) {
@@ -451,21 +459,43 @@ int launch_skinny_lds(hipStream_t st, int batch, const SkinnyLdsParams& p) {
     return hipGetLastError() == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
 }
 
+// k split of the streaming kernel: enough workgroups to cover the CUs, at
+// least 8 k-steps per wave, and a counter per column block.
+int skinny_k_split(int cus, int64_t wgs, int k) {
+    const int T = (k + 31) / 32;
+    int ks = 1;
+    while (wgs * ks * 2 <= cus && T / (ks * 2) >= kSkinnyKP * 8) ks *= 2;
+    if (wgs > static_cast<int64_t>(kSkinnyArrivalBytes / 4)) ks = 1;
+    return ks;
+}
+
+// Bytes of [arrival counters | k-split partials] the streaming kernel needs for
+// this shape on any device (the split is bounded by the k-step count alone).
+size_t skinny_ws_bytes(int m, int k, int64_t wgs) {
+    const int T = (k + 31) / 32;
+    int ks = 1;
+    while (T / (ks * 2) >= kSkinnyKP * 8) ks *= 2;
+    if (ks == 1 || wgs > static_cast<int64_t>(kSkinnyArrivalBytes / 4)) return 0;
+    const int MB = (m + 15) / 16;
+    return kSkinnyArrivalBytes + static_cast<size_t>(wgs) * ks * kSkinnyCB * MB * 256 * sizeof(float);
+}
+
+// ws: the skinny_ws_bytes() region (arrival counters zero between calls), or
+// NULL for the library's own.
 template <typename OT, bool RES>
-int launch_skinny(int dev, hipStream_t st, int batch, SkinnyParams p) {
+int launch_skinny(int dev, hipStream_t st, int batch, SkinnyParams p, uint8_t* ws = nullptr, size_t ws_bytes = 0) {
     const int ncb = p.cb_end[2];
     const int T = (p.k + 31) / 32;
     const int MB = (p.m + 15) / 16;
     const int64_t wgs = static_cast<int64_t>(ncb) * batch;
     const int cus = device_cu_count(dev) > 0 ? device_cu_count(dev) : 256;
-    int ks = 1;
-    while (wgs * ks * 2 <= cus && T / (ks * 2) >= kSkinnyKP * 8) ks *= 2;
-    if (wgs > static_cast<int64_t>(kSkinnyArrivalBytes / 4)) ks = 1;
+    const int ks = skinny_k_split(cus, wgs, p.k);
     p.ks_count = ks;
     p.slice = (T + ks - 1) / ks;
     if (ks > 1) {
-        const size_t part_bytes = static_cast<size_t>(wgs) * ks * kSkinnyCB * MB * 256 * sizeof(float);
-        uint8_t* ws = static_cast<uint8_t*>(device_workspace(dev, kSkinnyArrivalBytes + part_bytes, kWorkspaceSkinny));
+        const size_t need = kSkinnyArrivalBytes + static_cast<size_t>(wgs) * ks * kSkinnyCB * MB * 256 * sizeof(float);
+        if (!ws) ws = static_cast<uint8_t*>(device_workspace(dev, need, kWorkspaceSkinny));
+        else if (ws_bytes < need) return SUPERSONIC_ERR_WORKSPACE;
         if (!ws) return SUPERSONIC_ERR_WORKSPACE;
         p.arrivals = reinterpret_cast<unsigned*>(ws);
         p.part = reinterpret_cast<float*>(ws + kSkinnyArrivalBytes);
@@ -513,14 +543,16 @@ bool make_layout(hipblasLtMatrixLayout_t* l, uint64_t rows, uint64_t cols, int64
 }  // namespace
 
 // 0 on success, 1 when hipBLASLt has no plan for the shape, 2 on a launch error.
-int lt_gemm(int dev, hipStream_t st, int batch, int m, int n, int k, const void* lhs, const void* rhs, void* out) {
+// ws: kLtWorkspace bytes of caller memory, or NULL for the library's own.
+int lt_gemm(int dev, hipStream_t st, int batch, int m, int n, int k, const void* lhs, const void* rhs, void* out,
+            void* ws = nullptr) {
     std::lock_guard<std::mutex> lock(g_lt_mutex);
     LtDevice& D = g_lt[dev];
     if (!D.handle && hipblasLtCreate(&D.handle) != HIPBLAS_STATUS_SUCCESS) {
         D.handle = nullptr;
         return 1;
     }
-    void* ws = device_workspace(dev, kLtWorkspace, kWorkspaceProjLt);
+    if (!ws) ws = device_workspace(dev, kLtWorkspace, kWorkspaceProjLt);
     if (!ws) return 2;
     const auto key = std::make_tuple(batch, m, n, k);
     auto it = D.plans.find(key);
@@ -623,9 +655,44 @@ extern "C" int supersonic_qwen35_hip_element_add(int dtype, size_t device_ordina
     return 0;
 }
 
+namespace ssa {
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// Workspace of the o_proj entry point: the streaming kernel's [counters |
+// partials] (rows <= the streaming limit), or the GEMM output rows followed by
+// the hipBLASLt workspace.
+size_t o_proj_ws_bytes(int m, int n, int k) {
+    if (m <= skinny_max_m()) return skinny_ws_bytes(m, k, (n + kSkinnyCols - 1) / kSkinnyCols);
+    return align256(static_cast<size_t>(m) * n * 2) + kLtWorkspace;
+}
+// Workspace of the qkv entry point: the normed rows, then the streaming
+// kernel's [counters | partials] or the hipBLASLt workspace.
+size_t qkv_ws_bytes(int m, int k, int nq, int nkv) {
+    const size_t normed = align256(static_cast<size_t>(m) * k * 2);
+    if (m <= skinny_max_m()) return normed + skinny_ws_bytes(m, k, nq / kSkinnyCols + 2 * (nkv / kSkinnyCols));
+    return normed + kLtWorkspace;
+}
+}  // namespace ssa
+
+extern "C" size_t supersonic_attn_gfx950_o_proj_workspace_size(size_t rows, size_t hidden_dim, size_t attn_dim) {
+    if (rows == 0 || hidden_dim == 0 || rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || attn_dim > 0x7FFFFFFF)
+        return 0;
+    return o_proj_ws_bytes(static_cast<int>(rows), static_cast<int>(hidden_dim), static_cast<int>(attn_dim));
+}
+
+extern "C" size_t supersonic_attn_gfx950_qkv_proj_workspace_size(size_t rows, size_t hidden_dim, size_t q_out_dim,
+                                                                 size_t kv_out_dim) {
+    if (rows == 0 || rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || q_out_dim > 0x7FFFFFFF ||
+        kv_out_dim > 0x7FFFFFFF)
+        return 0;
+    return qkv_ws_bytes(static_cast<int>(rows), static_cast<int>(hidden_dim), static_cast<int>(q_out_dim),
+                        static_cast<int>(kv_out_dim));
+}
+
 extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, void* stream, int hidden_dtype,
                                                       size_t rows, size_t hidden_dim, size_t attn_dim,
-                                                      const void* attn, const void* o_proj_w, void* hidden) {
+                                                      const void* attn, const void* o_proj_w, void* hidden,
+                                                      void* workspace, size_t workspace_bytes) {
     if (hidden_dtype != SUPERSONIC_DTYPE_BF16 && hidden_dtype != SUPERSONIC_DTYPE_F32) return SUPERSONIC_ERR_DTYPE;
     if (rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || attn_dim > 0x7FFFFFFF) return SUPERSONIC_ERR_RANGE;
     if (rows == 0 || hidden_dim == 0) return 0;
@@ -635,6 +702,7 @@ extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, voi
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = static_cast<int>(rows), n = static_cast<int>(hidden_dim), k = static_cast<int>(attn_dim);
     const bool f32 = hidden_dtype == SUPERSONIC_DTYPE_F32;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
     const ProfileEvents ev = take_profile_events();
     if (ev.before) (void)hipEventRecord(ev.before, st);
     if (skinny_fits(m, k, attn, o_proj_w)) {
@@ -649,15 +717,26 @@ extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, voi
             rc = f32 ? launch_skinny_lds<float, true>(st, 1, lds_params(p))
                      : launch_skinny_lds<bf16_t, true>(st, 1, lds_params(p));
         else
-            rc = f32 ? launch_skinny<float, true>(dev, st, 1, p) : launch_skinny<bf16_t, true>(dev, st, 1, p);
+            rc = f32 ? launch_skinny<float, true>(dev, st, 1, p, ws, workspace_bytes)
+                     : launch_skinny<bf16_t, true>(dev, st, 1, p, ws, workspace_bytes);
         if (rc) return rc;
     } else {
         const size_t total = rows * hidden_dim;
-        void* y = device_workspace(dev, total * 2, kWorkspaceProj);
+        void* y;
+        void* lt_ws = nullptr;
+        if (ws) {
+            if (workspace_bytes < align256(total * 2) + kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
+            y = ws;
+            lt_ws = ws + align256(total * 2);
+        } else {
+            y = device_workspace(dev, total * 2, kWorkspaceProj);
+        }
         if (!y) return SUPERSONIC_ERR_WORKSPACE;
         if (k == 0) {
-            if (hipMemsetAsync(y, 0, total * 2, st) != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
-        } else if (lt_gemm(dev, st, 1, m, n, k, attn, o_proj_w, y) != 0) {
+            hipLaunchKernelGGL(fill_u16_kernel, dim3(stride_blocks(total)), dim3(256), 0, st, total,
+                               static_cast<uint16_t*>(y));
+            if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+        } else if (lt_gemm(dev, st, 1, m, n, k, attn, o_proj_w, y, lt_ws) != 0) {
             return SUPERSONIC_ERR_LAUNCH;
         }
         const dim3 grid(stride_blocks(total)), blk(256);
@@ -677,7 +756,7 @@ extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stre
                                                size_t hidden_dim, size_t q_out_dim, size_t kv_out_dim, float eps,
                                                const void* hidden, const void* input_norm_w, const void* q_proj_w,
                                                const void* k_proj_w, const void* v_proj_w, void* q_proj_out,
-                                               void* k_out, void* v_out) {
+                                               void* k_out, void* v_out, void* workspace, size_t workspace_bytes) {
     if (hidden_dtype != SUPERSONIC_DTYPE_BF16 && hidden_dtype != SUPERSONIC_DTYPE_F32) return SUPERSONIC_ERR_DTYPE;
     if (rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || q_out_dim > 0x7FFFFFFF || kv_out_dim > 0x7FFFFFFF)
         return SUPERSONIC_ERR_RANGE;
@@ -694,11 +773,24 @@ extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stre
     const bool aligned = ((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(input_norm_w) |
                            reinterpret_cast<uintptr_t>(q_proj_w) | reinterpret_cast<uintptr_t>(k_proj_w) |
                            reinterpret_cast<uintptr_t>(v_proj_w)) & 15) == 0;
+    // the normed rows go to the workspace once (bf16 [rows, hidden_dim]),
+    // followed by the projection's own workspace
+    const size_t normed_bytes = align256(static_cast<size_t>(m) * k * 2);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint16_t* normed;
+    uint8_t* rest = nullptr;
+    size_t rest_bytes = 0;
+    if (ws) {
+        if (workspace_bytes < normed_bytes) return SUPERSONIC_ERR_WORKSPACE;
+        normed = reinterpret_cast<uint16_t*>(ws);
+        rest = ws + normed_bytes;
+        rest_bytes = workspace_bytes - normed_bytes;
+    } else {
+        normed = static_cast<uint16_t*>(device_workspace(dev, static_cast<size_t>(m) * k * 2, kWorkspaceProj));
+    }
+    if (!normed) return SUPERSONIC_ERR_WORKSPACE;
     const ProfileEvents ev = take_profile_events();
     if (ev.before) (void)hipEventRecord(ev.before, st);
-    // the normed rows go to the workspace once (bf16 [rows, hidden_dim])
-    uint16_t* normed = static_cast<uint16_t*>(device_workspace(dev, static_cast<size_t>(m) * k * 2, kWorkspaceProj));
-    if (!normed) return SUPERSONIC_ERR_WORKSPACE;
     {
         const dim3 grid(m), blk(256);
         if (f32)
@@ -729,17 +821,18 @@ extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stre
         if (p.cb_end[2] > 0) {
             const int rc = lds_path(dev, m, k, 1, p.cb_end[2])
                                ? launch_skinny_lds<bf16_t, false>(st, 1, lds_params(p))
-                               : launch_skinny<bf16_t, false>(dev, st, 1, p);
+                               : launch_skinny<bf16_t, false>(dev, st, 1, p, rest, rest_bytes);
             if (rc) return rc;
         }
     } else {
         // GEMM-sized: one hipBLASLt GEMM per matrix
-        const void* ws[3] = {q_proj_w, k_proj_w, v_proj_w};
+        if (ws && rest_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
+        const void* wts[3] = {q_proj_w, k_proj_w, v_proj_w};
         void* os[3] = {q_proj_out, k_out, v_out};
         const int ns[3] = {nq, nkv, nkv};
         for (int i = 0; i < 3; ++i) {
             if (ns[i] == 0) continue;
-            if (lt_gemm(dev, st, 1, m, ns[i], k, normed, ws[i], os[i]) != 0) return SUPERSONIC_ERR_LAUNCH;
+            if (lt_gemm(dev, st, 1, m, ns[i], k, normed, wts[i], os[i], rest) != 0) return SUPERSONIC_ERR_LAUNCH;
         }
     }
     if (ev.after) (void)hipEventRecord(ev.after, st);

@@ -89,17 +89,22 @@ SIGNATURES = {
          _p, _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p, _p, _sz],
     "supersonic_attn_gfx950_decode_attend":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _f, _p, _p, C.POINTER(KvCacheDesc), _p, _p, _p, _sz],
+    "supersonic_attn_gfx950_prefill_workspace_size": [_i, _sz, _sz, _sz, _sz],
     "supersonic_attn_gfx950_prefill":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
-         _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p],
-    "supersonic_attn_gfx950_o_proj_residual": [_sz, _p, _i, _sz, _sz, _sz, _p, _p, _p],
-    "supersonic_attn_gfx950_qkv_proj": [_sz, _p, _i, _sz, _sz, _sz, _sz, _f, _p, _p, _p, _p, _p, _p, _p, _p],
+         _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p, _p, _sz],
+    "supersonic_attn_gfx950_o_proj_workspace_size": [_sz, _sz, _sz],
+    "supersonic_attn_gfx950_o_proj_residual": [_sz, _p, _i, _sz, _sz, _sz, _p, _p, _p, _p, _sz],
+    "supersonic_attn_gfx950_qkv_proj_workspace_size": [_sz, _sz, _sz, _sz],
+    "supersonic_attn_gfx950_qkv_proj":
+        [_sz, _p, _i, _sz, _sz, _sz, _sz, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "supersonic_attn_gfx950_set_profile_events": [_p, _p],
     "supersonic_attn_rope_tables": [_sz, _sz, C.c_double, _p, _p],
     "supersonic_attn_version": [],
 }
-RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
+RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_gfx950_prefill_workspace_size": _sz,
+            "supersonic_attn_gfx950_o_proj_workspace_size": _sz, "supersonic_attn_gfx950_qkv_proj_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
             "supersonic_attn_gfx950_set_profile_events": None}
 
 _LIB = None
@@ -312,9 +317,26 @@ def decode_attend(ordinal, q, kv_lens, cache: KvCache, out, *, q_heads, kv_heads
     _check("decode_attend", st)
 
 
+def _ws(workspace):
+    return _ptr(workspace), 0 if workspace is None else workspace.numel() * workspace.element_size()
+
+
+def prefill_workspace_size(fp8, kv_heads, head_dim, chunk_len, chunk_start) -> int:
+    return int(load().supersonic_attn_gfx950_prefill_workspace_size(KV_FP8_E4M3 if fp8 else KV_BF16, kv_heads,
+                                                                     head_dim, chunk_len, chunk_start))
+
+
+def o_proj_workspace_size(rows, hidden_dim, attn_dim) -> int:
+    return int(load().supersonic_attn_gfx950_o_proj_workspace_size(rows, hidden_dim, attn_dim))
+
+
+def qkv_proj_workspace_size(rows, hidden_dim, q_out_dim, kv_out_dim) -> int:
+    return int(load().supersonic_attn_gfx950_qkv_proj_workspace_size(rows, hidden_dim, q_out_dim, kv_out_dim))
+
+
 def fused_prefill(ordinal, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table, sin_table, cache: KvCache,
                   out, *, q_heads, kv_heads, head_dim, rotary_dim, chunk_start=0, eps=1e-6, scale=None,
-                  stream=None):
+                  stream=None, workspace=None):
     """``supersonic_attn_gfx950_prefill``: one prefill chunk of sequence 0 of ``cache``."""
     S = q_proj.shape[0]
     scale = head_dim ** -0.5 if scale is None else scale
@@ -322,11 +344,11 @@ def fused_prefill(ordinal, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table, 
     st = load().supersonic_attn_gfx950_prefill(
         ordinal, _stream_ptr(stream), KV_FP8_E4M3 if cache.fp8 else KV_BF16, q_heads, kv_heads, head_dim,
         rotary_dim, S, chunk_start, eps, scale, _ptr(q_proj), _ptr(k_new), _ptr(v_new), _ptr(q_norm_w),
-        _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), C.byref(desc), _ptr(out))
+        _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), C.byref(desc), _ptr(out), *_ws(workspace))
     _check("fused_prefill", st)
 
 
-def o_proj_residual(ordinal, attn, o_proj_w, hidden, stream=None):
+def o_proj_residual(ordinal, attn, o_proj_w, hidden, stream=None, workspace=None):
     """``hidden = bf16(hidden + bf16(attn . o_proj_w^T))`` in place; hidden bf16 or f32."""
     import torch
     rows, attn_dim = attn.shape
@@ -336,11 +358,12 @@ def o_proj_residual(ordinal, attn, o_proj_w, hidden, stream=None):
     assert attn.is_contiguous() and o_proj_w.is_contiguous() and hidden.is_contiguous()
     hd = {torch.bfloat16: ScalarType.BF16, torch.float32: ScalarType.F32}[hidden.dtype]
     _check("o_proj_residual", load().supersonic_attn_gfx950_o_proj_residual(
-        ordinal, _stream_ptr(stream), hd, rows, hidden_dim, attn_dim, _ptr(attn), _ptr(o_proj_w), _ptr(hidden)))
+        ordinal, _stream_ptr(stream), hd, rows, hidden_dim, attn_dim, _ptr(attn), _ptr(o_proj_w), _ptr(hidden),
+        *_ws(workspace)))
 
 
 def qkv_proj(ordinal, hidden, input_norm_w, q_proj_w, k_proj_w, v_proj_w, q_proj_out, k_out, v_out, eps=1e-6,
-             stream=None):
+             stream=None, workspace=None):
     """Input RMSNorm (1 + w) + Q/K/V projections: the fused decode's q_proj / k_new / v_new."""
     import torch
     rows, hid = hidden.shape
@@ -354,7 +377,8 @@ def qkv_proj(ordinal, hidden, input_norm_w, q_proj_w, k_proj_w, v_proj_w, q_proj
     hd = {torch.bfloat16: ScalarType.BF16, torch.float32: ScalarType.F32}[hidden.dtype]
     _check("qkv_proj", load().supersonic_attn_gfx950_qkv_proj(
         ordinal, _stream_ptr(stream), hd, rows, hid, nq, nkv, eps, _ptr(hidden), _ptr(input_norm_w),
-        _ptr(q_proj_w), _ptr(k_proj_w), _ptr(v_proj_w), _ptr(q_proj_out), _ptr(k_out), _ptr(v_out)))
+        _ptr(q_proj_w), _ptr(k_proj_w), _ptr(v_proj_w), _ptr(q_proj_out), _ptr(k_out), _ptr(v_out),
+        *_ws(workspace)))
 
 
 def quantize_kv_fp8_ocp(ordinal, src, dst_fp8, dst_scale, num_kv_heads, seq_len, head_dim, max_t, pos_offset,

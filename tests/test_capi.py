@@ -99,7 +99,7 @@ def test_fused_entry_validation(lib):
     assert dec(2, 256, 64) == K.ERR["CACHE"]         # pages must hold whole 16-token blocks
     desc.block_table = None
     pre = lambda kvd, hq, hkv, hd, rot: lib.supersonic_attn_gfx950_prefill(
-        0, None, kvd, hq, hkv, hd, rot, 16, 0, 1e-6, 0.0625, p, p, p, p, p, p, p, C.byref(desc), p)
+        0, None, kvd, hq, hkv, hd, rot, 16, 0, 1e-6, 0.0625, p, p, p, p, p, p, p, C.byref(desc), p, None, 0)
     assert pre(9, 16, 4, 256, 64) == K.ERR["DTYPE"]
     assert pre(2, 16, 5, 256, 64) == K.ERR["HEADS"]
     assert pre(2, 16, 4, 200, 64) == K.ERR["HEAD_DIM"]
@@ -112,14 +112,14 @@ def test_fused_entry_validation(lib):
 def test_projection_entry_validation(lib):
     p = 0x1000  # never dereferenced: validation fails first
     op = lambda hd, rows, hid, adim, attn=p, w=p, h=p: lib.supersonic_attn_gfx950_o_proj_residual(
-        0, None, hd, rows, hid, adim, attn, w, h)
+        0, None, hd, rows, hid, adim, attn, w, h, None, 0)
     assert op(0, 8, 64, 64) == K.ERR["DTYPE"]          # f16 hidden is not a reference layout
     assert op(2, 8, 64, 64, h=None) == K.ERR["NULL"]
     assert op(1, 8, 64, 64, w=None) == K.ERR["NULL"]
     assert op(2, 1 << 31, 64, 64) == K.ERR["RANGE"]
     assert op(2, 0, 64, 64, attn=None, w=None, h=None) == 0  # nothing to do
     qkv = lambda hd, hid, nq=64, nkv=16, x=p, kw=p: lib.supersonic_attn_gfx950_qkv_proj(
-        0, None, hd, 4, hid, nq, nkv, 1e-6, x, p, p, kw, p, p, p, p)
+        0, None, hd, 4, hid, nq, nkv, 1e-6, x, p, p, kw, p, p, p, p, None, 0)
     assert qkv(0, 64) == K.ERR["DTYPE"]
     assert qkv(2, 64, x=None) == K.ERR["NULL"]
     assert qkv(1, 64, kw=None) == K.ERR["NULL"]
@@ -131,6 +131,13 @@ def test_workspace_size_is_host_only(lib):
     n = K.decode_workspace_size(1, 16, 4, 256, 32769)
     assert n > 16 * 256 * 4
     assert K.decode_workspace_size(8, 16, 4, 256, 32769) >= n
+    # prefill: the V^T staging of every position (x2 with an fp8 cache)
+    assert K.prefill_workspace_size(False, 4, 256, 4096, 0) == 4 * 256 * 4096 * 2
+    assert K.prefill_workspace_size(True, 4, 256, 100, 30) == 2 * 4 * 256 * 192 * 2
+    # projections: decode rows need only the k-split counters/partials (or nothing)
+    assert K.o_proj_workspace_size(8, 4096, 4096) < (1 << 22)
+    assert K.qkv_proj_workspace_size(8, 4096, 8192, 1024) >= 8 * 4096 * 2
+    assert K.o_proj_workspace_size(100, 4096, 4096) >= 100 * 4096 * 2
 
 
 @pytest.mark.parametrize("rot,max_pos,theta", [(64, 70000, 1.0e7), (32, 4097, 1.0e4), (128, 513, 1.0e6)])

@@ -129,3 +129,72 @@ def test_prefill_graph_replays_match_eager():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {r}"
+
+
+def test_first_call_captured_with_caller_workspaces():
+    """Every entry point of a decode layer and a prefill chunk captured into a
+    graph on its FIRST call at a new size, with caller-owned workspaces (sized by
+    the *_workspace_size queries, zero-filled once): nothing is allocated or
+    synchronised inside the capture, and the replays agree with eager runs that
+    use the library's own workspaces."""
+    announce("first-call capture with caller workspaces")
+    B, Hq, Hkv, D, rot, hid, L = 2, 16, 4, 256, 64, 2048, 1500
+    s = torch.cuda.Stream()
+    d = decode_layer_inputs(B, Hq, Hkv, D, rot, hid, L, 95)
+    pos = torch.tensor([L, L - 7], dtype=torch.int32, device=DEV)
+    q_proj = torch.empty(B, Hq * 2 * D, dtype=torch.bfloat16, device=DEV)
+    k_new = torch.empty(B, Hkv * D, dtype=torch.bfloat16, device=DEV)
+    v_new = torch.empty_like(k_new)
+    attn = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    S, start = 200, 64
+    g0 = gen(96)
+    qp = O.randn_bf16(g0, S, Hq * 2 * D).to(DEV)
+    kr = O.randn_bf16(g0, S, Hkv * D).to(DEV)
+    vr = O.randn_bf16(g0, S, Hkv * D).to(DEV)
+    pout = torch.empty(S, Hq * D, dtype=torch.bfloat16, device=DEV)
+    zeros = lambda n: torch.zeros(max(int(n), 1), dtype=torch.uint8, device=DEV)
+    ws = dict(qkv=zeros(K.qkv_proj_workspace_size(B, hid, Hq * 2 * D, Hkv * D)),
+              dec=zeros(K.decode_workspace_size(B, Hq, Hkv, D, L + 1)),
+              op=zeros(K.o_proj_workspace_size(B, hid, Hq * D)),
+              pre=zeros(K.prefill_workspace_size(False, Hkv, D, S, start)))
+
+    def run(hidden, cache, pcache, use_ws):
+        w = ws if use_ws else {}
+        K.qkv_proj(0, hidden, d["nw"], d["wq"], d["wk"], d["wv"], q_proj, k_new, v_new, stream=s,
+                   workspace=w.get("qkv"))
+        K.fused_decode(0, q_proj, k_new, v_new, d["qw"], d["kw"], d["cos"], d["sin"], pos, cache, attn,
+                       q_heads=Hq, kv_heads=Hkv, head_dim=D, rotary_dim=rot, max_kv_len=L + 1, stream=s,
+                       workspace=w.get("dec"))
+        K.o_proj_residual(0, attn, d["wo"], hidden, stream=s, workspace=w.get("op"))
+        K.fused_prefill(0, qp, kr, vr, d["qw"], d["kw"], d["cos"], d["sin"], pcache, pout, q_heads=Hq,
+                        kv_heads=Hkv, head_dim=D, rotary_dim=rot, chunk_start=start, stream=s,
+                        workspace=w.get("pre"))
+
+    pk = O.randn_bf16(g0, 1, Hkv, start + S, D).to(DEV)
+    pv = O.randn_bf16(g0, 1, Hkv, start + S, D).to(DEV)
+    hidden = d["hidden"].clone()
+    cache = K.KvCache(d["kc"].clone(), d["vc"].clone())
+    pcache = K.KvCache(pk.clone(), pv.clone())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run(hidden, cache, pcache, True)
+    # eager reference with library-owned workspaces
+    e_hidden = d["hidden"].clone()
+    e_cache = K.KvCache(d["kc"].clone(), d["vc"].clone())
+    e_pcache = K.KvCache(pk.clone(), pv.clone())
+    with torch.cuda.stream(s):
+        run(e_hidden, e_cache, e_pcache, False)
+    s.synchronize()
+    e_attn, e_pout = attn.clone(), pout.clone()
+    for r in range(3):
+        hidden.copy_(d["hidden"])
+        attn.zero_()
+        pout.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close_ulps(attn, e_attn, f"replay {r}: attention", floor=2.0 ** -8)
+        assert_close_ulps(hidden, e_hidden, f"replay {r}: hidden", floor=2.0 ** -6)
+        assert torch.equal(pout, e_pout), f"replay {r}: prefill"
+        assert int(ws["dec"][:65536].count_nonzero()) == 0
