@@ -209,6 +209,23 @@ int supersonic_attn_gfx950_decode(
     const int32_t* positions, const supersonic_kv_cache* cache, void* out,
     void* workspace, size_t workspace_bytes);
 
+/* supersonic_attn_gfx950_decode without a workspace and without any allocation
+ * (no reference counterpart: for callers that cannot allocate device memory,
+ * e.g. code under HIP graph capture or serving loops that forbid hipMalloc).
+ * The split partials and arrival counters live in a file-scope device array of
+ * 8 MiB per GPU (held until the process ends); shapes whose
+ * supersonic_attn_gfx950_decode_workspace_size() exceeds 8 MiB return
+ * SUPERSONIC_ERR_WORKSPACE.  Every call on a GPU shares that array, so calls
+ * that overlap on one GPU (different streams, or threads) race.  Same
+ * arguments and results as supersonic_attn_gfx950_decode. */
+int supersonic_attn_gfx950_decode_noalloc(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
+    size_t max_kv_len, float eps, float scale,
+    const void* q_proj, const void* k_new, const void* v_new,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const int32_t* positions, const supersonic_kv_cache* cache, void* out);
+
 /* Attention-only decode over an existing cache: q [batch, Hq, D] bf16 (already
  * normalised and rotated), kv_lens [batch] int32 device, optional gate
  * [batch, Hq*D] bf16 (NULL = no gate), out [batch, Hq*D] bf16. */

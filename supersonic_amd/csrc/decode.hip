@@ -1122,6 +1122,65 @@ extern "C" int supersonic_attn_gfx950_decode(
     return run_decode(r);
 }
 
+// ----------------------------------------------------------------------------
+// Allocation-free decode: the split partials and arrival counters live in a
+// file-scope device array (one copy per GPU, held until the process ends)
+// instead of a caller or library workspace.
+// ----------------------------------------------------------------------------
+constexpr size_t kScratchBytes = 8u << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+__global__ void zero_u32_kernel(unsigned* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // device address of `scratch`, per device
+}  // namespace
+
+// Device address of this device's `scratch` (the current device must be
+// `device`), looked up once per device.  The first lookup on a device also
+// clears the arrival counters with a kernel on `st` (every later call leaves
+// them at zero).  NULL if the lookup fails.
+static void* scratch_for(int device, hipStream_t st) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0) return nullptr;
+    if (static_cast<size_t>(device) >= g_scratch_ptr.size()) g_scratch_ptr.resize(device + 1, nullptr);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, st, static_cast<unsigned*>(ptr), kMaxArrivals);
+        if (hipGetLastError() != hipSuccess) return nullptr;
+        g_scratch_ptr[device] = ptr;
+    }
+    return g_scratch_ptr[device];
+}
+
+extern "C" int supersonic_attn_gfx950_decode_noalloc(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
+    size_t max_kv_len, float eps, float scale,
+    const void* q_proj, const void* k_new, const void* v_new,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const int32_t* positions, const supersonic_kv_cache* cache, void* out) {
+    if (kv_dtype != SUPERSONIC_KV_BF16 && kv_dtype != SUPERSONIC_KV_FP8_E4M3) return SUPERSONIC_ERR_DTYPE;
+    if (int rc = check_sizes(batch, q_heads, kv_heads, head_dim, max_kv_len)) return rc;
+    if (kv_heads == 0) return SUPERSONIC_ERR_HEADS;
+    // shapes whose partials do not fit the scratch array are rejected up front
+    if (supersonic_attn_gfx950_decode_workspace_size(batch, q_heads, kv_heads, head_dim, max_kv_len) > kScratchBytes)
+        return SUPERSONIC_ERR_WORKSPACE;
+    void* ws;
+    {
+        ScopedDevice scoped(static_cast<int>(device_ordinal));
+        ws = scratch_for(static_cast<int>(device_ordinal), static_cast<hipStream_t>(stream));
+    }
+    if (!ws) return SUPERSONIC_ERR_WORKSPACE;
+    return supersonic_attn_gfx950_decode(device_ordinal, stream, kv_dtype, batch, q_heads, kv_heads, head_dim,
+                                         rotary_dim, max_kv_len, eps, scale, q_proj, k_new, v_new, q_norm_w,
+                                         k_norm_w, cos_table, sin_table, positions, cache, out, ws, kScratchBytes);
+}
+
 extern "C" int supersonic_attn_gfx950_decode_attend(
     size_t device_ordinal, void* stream, int kv_dtype,
     size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len,

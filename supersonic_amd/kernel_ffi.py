@@ -87,6 +87,9 @@ SIGNATURES = {
     "supersonic_attn_gfx950_decode":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
          _p, _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p, _p, _sz],
+    "supersonic_attn_gfx950_decode_noalloc":
+        [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
+         _p, _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p],
     "supersonic_attn_gfx950_decode_attend":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _f, _p, _p, C.POINTER(KvCacheDesc), _p, _p, _p, _sz],
     "supersonic_attn_gfx950_prefill_workspace_size": [_i, _sz, _sz, _sz, _sz],
@@ -302,6 +305,20 @@ def fused_decode(ordinal, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table, s
         _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), _ptr(positions), C.byref(desc), _ptr(out),
         _ptr(workspace), 0 if workspace is None else workspace.numel() * workspace.element_size())
     _check("fused_decode", st)
+
+
+def fused_decode_noalloc(ordinal, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table, sin_table, positions,
+                         cache: KvCache, out, *, q_heads, kv_heads, head_dim, rotary_dim, max_kv_len, eps=1e-6,
+                         scale=None, stream=None):
+    """``supersonic_attn_gfx950_decode_noalloc``: one decode step, no workspace, no allocation."""
+    B = q_proj.shape[0]
+    scale = head_dim ** -0.5 if scale is None else scale
+    desc = cache.desc()
+    st = load().supersonic_attn_gfx950_decode_noalloc(
+        ordinal, _stream_ptr(stream), KV_FP8_E4M3 if cache.fp8 else KV_BF16, B, q_heads, kv_heads, head_dim,
+        rotary_dim, max_kv_len, eps, scale, _ptr(q_proj), _ptr(k_new), _ptr(v_new), _ptr(q_norm_w),
+        _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), _ptr(positions), C.byref(desc), _ptr(out))
+    _check("fused_decode_noalloc", st)
 
 
 def decode_attend(ordinal, q, kv_lens, cache: KvCache, out, *, q_heads, kv_heads, head_dim, max_kv_len,
