@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
-    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|fp8|mixed|qkv|oproj|layer_graph|copy")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|prefill_fp8|fp8|mixed|qkv|oproj|layer_graph|copy")
     return ap.parse_args()
 
 
@@ -104,7 +104,7 @@ def main():
     if not args.skip_cpu:
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
-        out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "fp8", "mixed",
+        out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "prefill_fp8", "fp8", "mixed",
                                                           "qkv", "oproj", "layer_graph")}
     print(json.dumps(out))
 
@@ -284,6 +284,47 @@ class Workloads:
                 "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
                              "traffic": measured_traffic("prefill"), "kernel": "prefill_kernel"}}
+
+    def prefill_fp8(self):
+        """FP8 (OCP e4m3) KV lane of the fused prefill: a 4096-token chunk after a
+        4096-token cached prefix (Qwen3.5-9B shape, 16/4 heads, D 256).  The prefix
+        is read as codes x scale (bf16), the chunk unquantised; the chunk's K/V are
+        appended as e4m3 codes + scales.  Roofline of the MFMA attention kernel;
+        stage_ms = the rest of the step (the K/V staging pass: norm + RoPE + append
+        of the chunk, dequantised prefix K and V^T)."""
+        torch, K = self.torch, self.K
+        S, start, Hq, Hkv, D, rot = 4096, 4096, 16, 4, 256, 64
+        L = start + S
+        q_proj = self.randn(S, Hq * 2 * D, seed=31)
+        k_new = self.randn(S, Hkv * D, seed=32)
+        v_new = self.randn(S, Hkv * D, seed=33)
+        qw = (self.randn(D, seed=34).float() * 0.02 + 1).bfloat16()
+        kw = (self.randn(D, seed=35).float() * 0.02 + 1).bfloat16()
+        cos, sin = (t.to(self.dev) for t in K.rope_tables(rot, L + 1, 1.0e7))
+        kk = self.randn(1, Hkv, L, D, seed=36)
+        vv = self.randn(1, Hkv, L, D, seed=37)
+        ks = (kk.float().abs().amax(-1) / 448).clamp(min=1e-12)
+        vs = (vv.float().abs().amax(-1) / 448).clamp(min=1e-12)
+        kq = (kk.float() / ks[..., None]).to(torch.float8_e4m3fn).view(torch.uint8)
+        vq = (vv.float() / vs[..., None]).to(torch.float8_e4m3fn).view(torch.uint8)
+        del kk, vv
+        cache = K.KvCache(kq, vq, ks.contiguous(), vs.contiguous())
+        out = torch.empty(S, Hq * D, dtype=torch.bfloat16, device=self.dev)
+        ws = torch.zeros(K.prefill_workspace_size(True, Hkv, D, S, start), dtype=torch.uint8, device=self.dev)
+
+        def step(i):
+            K.fused_prefill(0, q_proj, k_new, v_new, qw, kw, cos, sin, cache, out, q_heads=Hq, kv_heads=Hkv,
+                            head_dim=D, rotary_dim=rot, chunk_start=start, workspace=ws)
+        step_ms, kern_ms, _ = self.timed(step)
+        fl = self.causal_flops(S, Hq, D, start)
+        ach = fl / (kern_ms * 1e-3) / 1e12
+        torch.cuda.empty_cache()
+        return {"workload": "FP8 e4m3 KV prefill: 4096-token chunk after a 4096-token fp8 prefix, 16/4 heads, D 256",
+                "tflops_step": fl / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms, "kernel_ms": kern_ms,
+                "stage_ms": step_ms - kern_ms, "flops": fl,
+                "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                             "kernel": "prefill_kernel (bf16 MFMA over the dequantised prefix)"}}
 
     def mixed(self):
         """Config 5: one 8192-token prefill chunk + 32 decode sequences, 16/2 heads,
