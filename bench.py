@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
-    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|prefill_fp8|fp8|mixed|qkv|oproj|layer_graph|copy")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|prefill_fp8|fp8|mixed|qkv|qkv_rope|oproj|layer_graph|copy")
     return ap.parse_args()
 
 
@@ -105,7 +105,7 @@ def main():
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
         out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "prefill_fp8", "fp8", "mixed",
-                                                          "qkv", "oproj", "layer_graph")}
+                                                          "qkv", "qkv_rope", "oproj", "layer_graph")}
     print(json.dumps(out))
 
 
@@ -406,6 +406,43 @@ class Workloads:
                              "frac": round(ach / HBM_PEAK_GBS, 4),
                              "traffic": measured_traffic("qkv"),  # the projection kernel's bytes (the norm kernel: 128 KB)
                              "kernel": "input_norm_kernel + skinny_lds_kernel (3 segments), events around both",
+                             "bytes_per_launch": kern_bytes}}
+
+    def qkv_rope(self):
+        """The fused projection of a config-2 decode step: input norm + Q/K/V
+        projections + per-head QK RMSNorm + partial RoPE + bf16 KV append (8 rows,
+        hidden 4096, 16/4 heads, D 256), 4 weight copies rotating past the MALL."""
+        torch, K = self.torch, self.K
+        rows, hid, Hq, Hkv, D, rot, copies, L = 8, 4096, 16, 4, 256, 64, 4, 32768
+        nq, nkv = Hq * 2 * D, Hkv * D
+        ws = [[(self.randn(n, hid, seed=60 + 3 * c + i) * (hid ** -0.5)).to(torch.bfloat16).contiguous()
+               for i, n in enumerate((nq, nkv, nkv))] for c in range(copies)]
+        hidden = self.randn(rows, hid, seed=70)
+        nwb = (self.randn(hid, seed=71) * 0.1).to(torch.bfloat16)
+        qw = (self.randn(D, seed=72).float() * 0.02 + 1).bfloat16()
+        kw = (self.randn(D, seed=73).float() * 0.02 + 1).bfloat16()
+        cos, sin = (t.to(self.dev) for t in K.rope_tables(rot, L + 1, 1.0e7))
+        pos = torch.full((rows,), L, dtype=torch.int32, device=self.dev)
+        cache = K.KvCache(torch.zeros(rows, Hkv, 64, D, dtype=torch.bfloat16, device=self.dev),
+                          torch.zeros(rows, Hkv, 64, D, dtype=torch.bfloat16, device=self.dev),
+                          block_table=torch.zeros(rows, L // 64 + 1, dtype=torch.int32, device=self.dev))
+        mk = lambda n: torch.empty(rows, n, dtype=torch.bfloat16, device=self.dev)
+        q, gate, k, v = mk(Hq * D), mk(Hq * D), mk(nkv), mk(nkv)
+        wsp = torch.zeros(K.qkv_proj_rope_workspace_size(rows, hid, Hq, Hkv, D), dtype=torch.uint8, device=self.dev)
+
+        def step(i):
+            K.qkv_proj_rope(0, hidden, nwb, *ws[i], qw, kw, cos, sin, pos, q, gate, k, v, q_heads=Hq, kv_heads=Hkv,
+                            head_dim=D, rotary_dim=rot, cache=cache, workspace=wsp)
+        step_ms, kern_ms, _ = self.timed(step, copies)
+        kern_bytes = (nq + 2 * nkv) * hid * 2 + rows * hid * 2 + hid * 2 + rows * (nq + 2 * nkv) * 2
+        ach = kern_bytes / (kern_ms * 1e-3) / 1e9
+        del ws
+        torch.cuda.empty_cache()
+        return {"workload": "input norm + Q/K/V projections + QK norm + RoPE + KV append, 8 rows, 4096 -> 16/4 heads",
+                "ms_per_step": step_ms, "kernel_ms": kern_ms, "bytes": kern_bytes,
+                "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                             "kernel": "input_norm_kernel + skinny_lds_kernel (fused norm/RoPE epilogue), events around both",
                              "bytes_per_launch": kern_bytes}}
 
     def layer_graph(self):

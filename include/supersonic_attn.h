@@ -289,6 +289,35 @@ int supersonic_attn_gfx950_qkv_proj(
     const void* q_proj_w, const void* k_proj_w, const void* v_proj_w, void* q_proj_out,
     void* k_out, void* v_out, void* workspace, size_t workspace_bytes);
 
+/* Input RMSNorm + Q/K/V projections + per-head Q/K RMSNorm ((1+w), qk_eps) +
+ * partial RoPE at positions[r] (+ KV-cache append), the megakernel's steps A-D
+ * (full_attention_4b.hip:4942-5101 feeding :5142-5224 and the append
+ * :5282-5294), and rms_norm_rows_model + matmul_proj + the norm/RoPE chain of
+ * prefill_engine.rs:1951-2096 for one position per row:
+ *   q_out [rows, q_heads*D]  normalised + rotated q of each head,
+ *   gate_out [rows, q_heads*D] the raw gate half of each q_proj head,
+ *   k_out [rows, kv_heads*D] normalised + rotated k, v_out [rows, kv_heads*D] v,
+ * all bf16; cache (NULL: none) is a bf16 cache view that receives k_out / v_out
+ * of row r at slot positions[r] of sequence r.  The outputs feed
+ * supersonic_attn_gfx950_decode_attend (q, gate, kv_lens = positions + 1).
+ * Rows <= 12 with rows * hidden_dim <= 32768 and head_dim 128/256: one
+ * weight-streaming launch whose epilogue normalises and rotates each head as
+ * its last column block completes; otherwise the projections, then one wave
+ * per (row, head).  workspace: at least
+ * supersonic_attn_gfx950_qkv_proj_rope_workspace_size() bytes, zero-filled
+ * before first use (per-head arrival counters left at zero by every call),
+ * or NULL for a library-owned buffer.  Status: SUPERSONIC_ERR_CACHE for an
+ * fp8 cache. */
+size_t supersonic_attn_gfx950_qkv_proj_rope_workspace_size(
+    size_t rows, size_t hidden_dim, size_t q_heads, size_t kv_heads, size_t head_dim);
+int supersonic_attn_gfx950_qkv_proj_rope(
+    size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim,
+    size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim, float eps, float qk_eps,
+    const void* hidden, const void* input_norm_w, const void* q_proj_w, const void* k_proj_w,
+    const void* v_proj_w, const void* q_norm_w, const void* k_norm_w, const void* cos_table,
+    const void* sin_table, const int32_t* positions, void* q_out, void* gate_out, void* k_out,
+    void* v_out, const supersonic_kv_cache* cache, void* workspace, size_t workspace_bytes);
+
 /* Output projection with the residual add, after the gated attention:
  *   hidden[r, j] = bf16(hidden[r, j] + bf16(sum_c attn[r, c] * o_proj_w[j, c]))
  * attn [rows, attn_dim] bf16 (the fused decode/prefill `out`), o_proj_w

@@ -32,11 +32,13 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdlib>
+#include <type_traits>
 #include <map>
 #include <mutex>
 #include <tuple>
 
 #include "common.hpp"
+#include "kv_view.hpp"
 #include "supersonic_attn.h"
 
 namespace ssa {
@@ -266,6 +268,69 @@ constexpr int kXsMax = 32768;  // staged elements (64 KB): two workgroups per CU
 constexpr int kXsChunks = kXsMax / 8 / 512;  // 16-byte chunks per thread at most
 constexpr int kXsDummy = kXsMax + 120;        // 16-byte slot for the chunks past the rows
 
+// Per-head QK RMSNorm + partial RoPE (+ KV-cache append) applied to the
+// Q/K projection outputs (the fused projection of the decode step).
+struct RopeEpi {
+    uint16_t* q_out;      // [m, Hq*D]   normalised + rotated q
+    uint16_t* gate_out;   // [m, Hq*D]   raw gate half of each q_proj head
+    uint16_t* k_out;      // [m, Hkv*D]  normalised + rotated k
+    uint16_t* v_out;      // [m, Hkv*D]
+    const uint16_t* q_norm_w;
+    const uint16_t* k_norm_w;
+    const uint16_t* cos_t;  // [max_pos, half_rot]
+    const uint16_t* sin_t;
+    const int32_t* pos;     // [m] position of each row (RoPE angle, cache slot)
+    KvView kv;              // bf16 cache the new k / v are appended to (kv.k == NULL: none)
+    unsigned* counters;     // [Hq + Hkv] column-block arrivals per head, zero between calls
+    int Hq, Hkv, D, half_rot;
+    float eps;
+};
+
+__device__ __forceinline__ void store_agent_u32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One head row of D bf16 values, lane holding the EPL = D / 64 consecutive
+// dims lane * EPL ..: RMSNorm with (1 + w) (bf16 result), then rotate-half
+// RoPE on dims [0, 2 hr) at position pos (bf16 result), the megakernel's
+// steps B-C (full_attention_4b.hip:5142-5224).  rowbuf: D floats of LDS
+// private to the wave (RoPE partners).
+template <int EPL>
+__device__ __forceinline__ void norm_rope_row(float (&x)[EPL], const uint16_t* w, const uint16_t* cos_t,
+                                              const uint16_t* sin_t, int pos, int hr, float eps, int D,
+                                              float* rowbuf) {
+    const int lane = threadIdx.x & 63;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) ss += x[j] * x[j];
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+        x[j] = bf16_round(x[j] * inv * (bf16_bits_to_f32(w[lane * EPL + j]) + 1.0f));
+    if (hr > 0) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) rowbuf[lane * EPL + j] = x[j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int d = lane * EPL + j;
+            if (d < 2 * hr) {
+                const int ti = d < hr ? d : d - hr;
+                const float c = bf16_bits_to_f32(cos_t[static_cast<int64_t>(pos) * hr + ti]);
+                const float sn = bf16_bits_to_f32(sin_t[static_cast<int64_t>(pos) * hr + ti]);
+                const float other = rowbuf[d < hr ? d + hr : d - hr];
+                x[j] = d < hr ? bf16_round(x[j] * c - other * sn) : bf16_round(other * sn + x[j] * c);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 struct SkinnyLdsParams {
     const uint16_t* x;      // [batch][m][k] bf16
     const uint16_t* w[3];
@@ -277,8 +342,8 @@ struct SkinnyLdsParams {
     int64_t x_bs, w_bs, o_bs;
 };
 
-template <typename OT, bool RES>
-__global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_eu(4))) void skinny_lds_kernel(SkinnyLdsParams p) {
+template <typename OT, bool RES, bool ROPE = false>
+__global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_eu(4))) void skinny_lds_kernel(SkinnyLdsParams p, RopeEpi e) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[kXsMax + 16 * 8];
     __shared__ __attribute__((aligned(16))) float red[kSkinnyWaves][256];
     const int tid = threadIdx.x;
@@ -357,16 +422,167 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][(4 * (lane >> 4) + i) * 16 + col] = acc[i];
     __syncthreads();
-    if (tid < 256) {
-        const int row = tid >> 4, c = cbs * 16 + (tid & 15);
-        if (row < m && c < n) {
+    if constexpr (!ROPE) {
+        if (tid < 256) {
+            const int row = tid >> 4, c = cbs * 16 + (tid & 15);
+            if (row < m && c < n) {
+                float sum = 0.f;
+#pragma unroll
+                for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][tid];
+                float y = bf16_round(sum);
+                const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * n + c;
+                if constexpr (RES) y = bf16_round(load_f32<OT>(static_cast<const OT*>(p.res), o) + y);
+                store_f32<OT>(static_cast<OT*>(p.out[seg]), o, y);
+            }
+        }
+    } else {
+        // Segments: 0 = W_q (per head [q | gate], 2D columns), 1 = W_k, 2 = W_v.
+        // A 16-column block lies inside one head and one half of it.
+        const int D = e.D;
+        const int c0 = cbs * 16;
+        const int hq = seg == 0 ? c0 / (2 * D) : c0 / D;   // head of the block
+        const bool is_q = seg == 0 && (c0 % (2 * D)) < D;
+        const bool is_gate = seg == 0 && !is_q;
+        const bool norm_block = is_q || seg == 1;           // its head is normalised once complete
+        if (tid < 256) {
+            const int row = tid >> 4, cc = tid & 15;
             float sum = 0.f;
 #pragma unroll
             for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][tid];
-            float y = bf16_round(sum);
-            const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * n + c;
-            if constexpr (RES) y = bf16_round(load_f32<OT>(static_cast<const OT*>(p.res), o) + y);
-            store_f32<OT>(static_cast<OT*>(p.out[seg]), o, y);
+            const uint32_t yb = f32_to_bf16_bits(sum);          // the projection's bf16 rounding
+            const uint32_t pair = yb | (static_cast<uint32_t>(__shfl_xor(static_cast<int>(yb), 1)) << 16);
+            if (row < m) {
+                const int d = (seg == 0 ? c0 % (2 * D) : c0 % D) + cc - (is_gate ? D : 0);
+                const int64_t hd = static_cast<int64_t>(row) * (seg == 0 ? e.Hq : e.Hkv) * D + hq * D + d;
+                if (norm_block) {
+                    // pre-norm values, device-coherent: the head's last block reads them back
+                    uint16_t* dst = seg == 0 ? e.q_out : e.k_out;
+                    if ((cc & 1) == 0) store_agent_u32(reinterpret_cast<uint32_t*>(dst + hd), pair);
+                } else if (is_gate) {
+                    e.gate_out[hd] = static_cast<uint16_t>(yb);
+                } else {
+                    e.v_out[hd] = static_cast<uint16_t>(yb);
+                    if (e.kv.k) {
+                        const int64_t o = e.kv.row(row, hq, e.pos[row], D) + d;
+                        reinterpret_cast<uint16_t*>(e.kv.v)[o] = static_cast<uint16_t>(yb);
+                    }
+                }
+            }
+        }
+        if (!norm_block) return;
+        // the head's last column block to arrive normalises and rotates it
+        __shared__ int last_s;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+        __syncthreads();
+        const int ctr = seg == 0 ? hq : e.Hq + hq;
+        if (tid == 0) {
+            const unsigned prev = atomicAdd(&e.counters[ctr], 1u);
+            last_s = prev == static_cast<unsigned>(D / 16 - 1);
+            if (last_s) e.counters[ctr] = 0u;  // every block of the head has arrived
+        }
+        __syncthreads();
+        if (!last_s) return;
+        float* rowbuf = reinterpret_cast<float*>(xs) + wave * D;  // the activations are no longer read
+        uint16_t* dst = seg == 0 ? e.q_out : e.k_out;
+        const uint16_t* nw = seg == 0 ? e.q_norm_w : e.k_norm_w;
+        const int H = seg == 0 ? e.Hq : e.Hkv;
+        for (int row = wave; row < m; row += kSkinnyWaves) {
+            uint16_t* rp = dst + static_cast<int64_t>(row) * H * D + hq * D;
+            const int pos = e.pos[row];
+            auto run = [&](auto epl_tag) {
+                constexpr int EPL = decltype(epl_tag)::value;
+                float x[EPL];
+                if constexpr (EPL == 4) {
+                    const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(rp) + lane, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[j] = bf16_bits_to_f32(static_cast<uint32_t>(v >> (16 * j)) & 0xFFFFu);
+                } else {
+                    const uint32_t v = __hip_atomic_load(reinterpret_cast<uint32_t*>(rp) + lane, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    x[0] = bf16_bits_to_f32(v & 0xFFFFu);
+                    x[1] = bf16_bits_to_f32(v >> 16);
+                }
+                norm_rope_row<EPL>(x, nw, e.cos_t, e.sin_t, pos, e.half_rot, e.eps, D, rowbuf);
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) {
+                    rp[lane * EPL + j] = static_cast<uint16_t>(f32_to_bf16_bits(x[j]));
+                    if (seg == 1 && e.kv.k) {
+                        const int64_t o = e.kv.row(row, hq, pos, D) + lane * EPL + j;
+                        reinterpret_cast<uint16_t*>(e.kv.k)[o] = static_cast<uint16_t>(f32_to_bf16_bits(x[j]));
+                    }
+                }
+            };
+            if (D == 256) run(std::integral_constant<int, 4>{});
+            else run(std::integral_constant<int, 2>{});
+        }
+    }
+}
+
+// Unfused path of the same epilogue (rows past the LDS-staged kernel, head
+// dims other than 128/256): one wave per (row, head) over the plain
+// projection outputs.  Blocks 0 .. Hq-1 of a row: q head (q_proj [m, Hq*2D]
+// -> q_out, gate_out); blocks Hq .. Hq+Hkv-1: kv head (k_in -> k_out
+// normalised + rotated, v_in -> v_out, cache append).
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(const uint16_t* q_proj, const uint16_t* k_in,
+                                                          const uint16_t* v_in, RopeEpi e) {
+    __shared__ float rowbuf[512];
+    const int row = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
+    const int D = e.D, pos = e.pos[row];
+    const bool qh = hh < e.Hq;
+    const int h = qh ? hh : hh - e.Hq;
+    const uint16_t* src = qh ? q_proj + (static_cast<int64_t>(row) * e.Hq + h) * 2 * D
+                             : k_in + (static_cast<int64_t>(row) * e.Hkv + h) * D;
+    uint16_t* dst = qh ? e.q_out + (static_cast<int64_t>(row) * e.Hq + h) * D
+                       : e.k_out + (static_cast<int64_t>(row) * e.Hkv + h) * D;
+    constexpr int EPL = 8;  // D <= 512: lane holds dims lane * 8 .. (lanes past D/8 idle)
+    const int active = D / 8;
+    float x[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) x[j] = lane < active ? bf16_bits_to_f32(src[lane * EPL + j]) : 0.f;
+    // norm_rope_row over D dims with lane-contiguous groups of 8
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) ss += x[j] * x[j];
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss / static_cast<float>(D) + e.eps);
+    const uint16_t* w = qh ? e.q_norm_w : e.k_norm_w;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+        if (lane < active) x[j] = bf16_round(x[j] * inv * (bf16_bits_to_f32(w[lane * EPL + j]) + 1.0f));
+    const int hr = e.half_rot;
+    if (hr > 0) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j)
+            if (lane < active) rowbuf[lane * EPL + j] = x[j];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int d = lane * EPL + j;
+            if (lane < active && d < 2 * hr) {
+                const int ti = d < hr ? d : d - hr;
+                const float c = bf16_bits_to_f32(e.cos_t[static_cast<int64_t>(pos) * hr + ti]);
+                const float sn = bf16_bits_to_f32(e.sin_t[static_cast<int64_t>(pos) * hr + ti]);
+                const float other = rowbuf[d < hr ? d + hr : d - hr];
+                x[j] = d < hr ? bf16_round(x[j] * c - other * sn) : bf16_round(other * sn + x[j] * c);
+            }
+        }
+    }
+    if (lane >= active) return;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int d = lane * EPL + j;
+        dst[d] = static_cast<uint16_t>(f32_to_bf16_bits(x[j]));
+        if (qh) {
+            e.gate_out[(static_cast<int64_t>(row) * e.Hq + h) * D + d] = src[D + d];
+        } else {
+            const uint16_t vv = v_in[(static_cast<int64_t>(row) * e.Hkv + h) * D + d];
+            e.v_out[(static_cast<int64_t>(row) * e.Hkv + h) * D + d] = vv;
+            if (e.kv.k) {
+                const int64_t o = e.kv.row(row, h, pos, D) + d;
+                reinterpret_cast<uint16_t*>(e.kv.k)[o] = static_cast<uint16_t>(f32_to_bf16_bits(x[j]));
+                reinterpret_cast<uint16_t*>(e.kv.v)[o] = vv;
+            }
         }
     }
 }
@@ -455,7 +671,7 @@ SkinnyLdsParams lds_params(const SkinnyParams& q) {
 template <typename OT, bool RES>
 int launch_skinny_lds(hipStream_t st, int batch, const SkinnyLdsParams& p) {
     const dim3 grid(p.cb_end[2], 1, batch), blk(64 * kSkinnyWaves);
-    hipLaunchKernelGGL((skinny_lds_kernel<OT, RES>), grid, blk, 0, st, p);
+    hipLaunchKernelGGL((skinny_lds_kernel<OT, RES, false>), grid, blk, 0, st, p, RopeEpi{});
     return hipGetLastError() == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
 }
 
@@ -834,6 +1050,166 @@ extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stre
             if (ns[i] == 0) continue;
             if (lt_gemm(dev, st, 1, m, ns[i], k, normed, wts[i], os[i], rest) != 0) return SUPERSONIC_ERR_LAUNCH;
         }
+    }
+    if (ev.after) (void)hipEventRecord(ev.after, st);
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Input RMSNorm + Q/K/V projections + per-head QK RMSNorm + partial RoPE
+// (+ bf16 KV-cache append): the megakernel's steps A-D
+// (full_attention_4b.hip:4942-5101 feeding :5142-5224, :5282-5294) in one
+// weight-streaming launch after the input norm.
+// ---------------------------------------------------------------------------
+namespace ssa {
+constexpr size_t kRopeCounterBytes = 64 << 10;  // per-head arrival counters (Hq + Hkv <= 16384)
+
+size_t qkv_rope_ws_bytes(int m, int k, int Hq, int Hkv, int D) {
+    const size_t normed = align256(static_cast<size_t>(m) * k * 2);
+    // unfused path: q_proj and the raw k / v rows, then the projection's own workspace
+    const size_t raw = align256(static_cast<size_t>(m) * Hq * 2 * D * 2) + 2 * align256(static_cast<size_t>(m) * Hkv * D * 2);
+    return kRopeCounterBytes + normed + raw + qkv_ws_bytes(m, k, Hq * 2 * D, Hkv * D) - align256(static_cast<size_t>(m) * k * 2);
+}
+}  // namespace ssa
+
+extern "C" size_t supersonic_attn_gfx950_qkv_proj_rope_workspace_size(size_t rows, size_t hidden_dim, size_t q_heads,
+                                                                      size_t kv_heads, size_t head_dim) {
+    if (rows == 0 || rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || q_heads > 4096 || kv_heads > 4096 ||
+        head_dim > 512)
+        return 0;
+    return qkv_rope_ws_bytes(static_cast<int>(rows), static_cast<int>(hidden_dim), static_cast<int>(q_heads),
+                             static_cast<int>(kv_heads), static_cast<int>(head_dim));
+}
+
+extern "C" int supersonic_attn_gfx950_qkv_proj_rope(
+    size_t device_ordinal, void* stream, int hidden_dtype, size_t rows, size_t hidden_dim, size_t q_heads,
+    size_t kv_heads, size_t head_dim, size_t rotary_dim, float eps, float qk_eps, const void* hidden,
+    const void* input_norm_w, const void* q_proj_w, const void* k_proj_w, const void* v_proj_w,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const int32_t* positions, void* q_out, void* gate_out, void* k_out, void* v_out,
+    const supersonic_kv_cache* cache, void* workspace, size_t workspace_bytes) {
+    if (hidden_dtype != SUPERSONIC_DTYPE_BF16 && hidden_dtype != SUPERSONIC_DTYPE_F32) return SUPERSONIC_ERR_DTYPE;
+    if (rows > 0x7FFFFFFF || hidden_dim > 0x7FFFFFFF || q_heads > 4096 || kv_heads > 4096) return SUPERSONIC_ERR_RANGE;
+    if (head_dim == 0 || head_dim > 512 || head_dim % 16 != 0) return SUPERSONIC_ERR_HEAD_DIM;
+    if (kv_heads == 0 || q_heads % kv_heads != 0) return SUPERSONIC_ERR_HEADS;
+    if (rotary_dim % 2 != 0 || rotary_dim > head_dim) return SUPERSONIC_ERR_ROTARY;
+    if (rows == 0) return 0;
+    if (!hidden || !input_norm_w || !q_proj_w || !k_proj_w || !v_proj_w || !q_norm_w || !k_norm_w || !positions ||
+        !q_out || !gate_out || !k_out || !v_out)
+        return SUPERSONIC_ERR_NULL;
+    if (rotary_dim > 0 && (!cos_table || !sin_table)) return SUPERSONIC_ERR_NULL;
+    if (hidden_dim == 0 || hidden_dim % 8 != 0) return SUPERSONIC_ERR_RANGE;
+    KvView kv{};
+    if (cache) {
+        if (cache->k_scale || cache->v_scale) return SUPERSONIC_ERR_CACHE;  // bf16 caches only
+        if (int rc = make_view(cache, false, &kv)) return rc;
+    }
+    const int dev = static_cast<int>(device_ordinal);
+    ScopedDevice scoped(dev);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int m = static_cast<int>(rows), k = static_cast<int>(hidden_dim);
+    const int Hq = static_cast<int>(q_heads), Hkv = static_cast<int>(kv_heads), D = static_cast<int>(head_dim);
+    const int nq = Hq * 2 * D, nkv = Hkv * D;
+    const size_t need = qkv_rope_ws_bytes(m, k, Hq, Hkv, D);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (ws) {
+        if (workspace_bytes < need) return SUPERSONIC_ERR_WORKSPACE;
+    } else {
+        // zero-filled once; every call leaves the counters at zero
+        ws = static_cast<uint8_t*>(device_workspace(dev, need, kWorkspaceProj));
+        if (!ws) return SUPERSONIC_ERR_WORKSPACE;
+    }
+    RopeEpi e{};
+    e.q_out = static_cast<uint16_t*>(q_out);
+    e.gate_out = static_cast<uint16_t*>(gate_out);
+    e.k_out = static_cast<uint16_t*>(k_out);
+    e.v_out = static_cast<uint16_t*>(v_out);
+    e.q_norm_w = static_cast<const uint16_t*>(q_norm_w);
+    e.k_norm_w = static_cast<const uint16_t*>(k_norm_w);
+    e.cos_t = static_cast<const uint16_t*>(cos_table);
+    e.sin_t = static_cast<const uint16_t*>(sin_table);
+    e.pos = positions;
+    e.kv = kv;
+    e.counters = reinterpret_cast<unsigned*>(ws);
+    e.Hq = Hq;
+    e.Hkv = Hkv;
+    e.D = D;
+    e.half_rot = static_cast<int>(rotary_dim / 2);
+    e.eps = qk_eps;
+    uint16_t* normed = reinterpret_cast<uint16_t*>(ws + kRopeCounterBytes);
+    uint8_t* rest = ws + kRopeCounterBytes + align256(static_cast<size_t>(m) * k * 2);
+    const bool f32 = hidden_dtype == SUPERSONIC_DTYPE_F32;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(input_norm_w) |
+                           reinterpret_cast<uintptr_t>(q_proj_w) | reinterpret_cast<uintptr_t>(k_proj_w) |
+                           reinterpret_cast<uintptr_t>(v_proj_w) | reinterpret_cast<uintptr_t>(q_out) |
+                           reinterpret_cast<uintptr_t>(k_out)) & 15) == 0;
+    const ProfileEvents ev = take_profile_events();
+    if (ev.before) (void)hipEventRecord(ev.before, st);
+    {
+        const dim3 grid(m), blk(256);
+        if (f32)
+            hipLaunchKernelGGL((input_norm_kernel<float>), grid, blk, 0, st, m, k, eps, static_cast<const float*>(hidden),
+                               static_cast<const uint16_t*>(input_norm_w), normed);
+        else
+            hipLaunchKernelGGL((input_norm_kernel<bf16_t>), grid, blk, 0, st, m, k, eps,
+                               static_cast<const bf16_t*>(hidden), static_cast<const uint16_t*>(input_norm_w), normed);
+        if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    }
+    const int ncb = (nq + 2 * nkv) / kSkinnyCols;
+    if (aligned && (D == 128 || D == 256) && lds_path(dev, m, k, 1, ncb) && m <= skinny_max_m() &&
+        Hq + Hkv <= static_cast<int>(kRopeCounterBytes / 4)) {
+        SkinnyLdsParams p{};
+        p.x = normed;
+        p.w[0] = static_cast<const uint16_t*>(q_proj_w);
+        p.w[1] = static_cast<const uint16_t*>(k_proj_w);
+        p.w[2] = static_cast<const uint16_t*>(v_proj_w);
+        p.n_seg[0] = nq;
+        p.n_seg[1] = p.n_seg[2] = nkv;
+        p.cb_end[0] = nq / kSkinnyCols;
+        p.cb_end[1] = p.cb_end[0] + nkv / kSkinnyCols;
+        p.cb_end[2] = p.cb_end[1] + nkv / kSkinnyCols;
+        p.m = m;
+        p.k = k;
+        hipLaunchKernelGGL((skinny_lds_kernel<bf16_t, false, true>), dim3(ncb, 1, 1), dim3(64 * kSkinnyWaves), 0, st,
+                           p, e);
+        if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
+    } else {
+        // plain projections into the workspace, then one wave per (row, head)
+        uint16_t* qp = reinterpret_cast<uint16_t*>(rest);
+        uint16_t* kr = reinterpret_cast<uint16_t*>(rest + align256(static_cast<size_t>(m) * nq * 2));
+        uint16_t* vr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(kr) + align256(static_cast<size_t>(m) * nkv * 2));
+        uint8_t* pws = reinterpret_cast<uint8_t*>(vr) + align256(static_cast<size_t>(m) * nkv * 2);
+        const size_t pws_bytes = ws + need > pws ? static_cast<size_t>(ws + need - pws) : 0;
+        if (skinny_fits(m, k, normed, q_proj_w) && aligned && nq % kSkinnyCols == 0 && nkv % kSkinnyCols == 0) {
+            SkinnyParams p{};
+            p.x = normed;
+            p.w[0] = static_cast<const uint16_t*>(q_proj_w);
+            p.w[1] = static_cast<const uint16_t*>(k_proj_w);
+            p.w[2] = static_cast<const uint16_t*>(v_proj_w);
+            p.out[0] = qp;
+            p.out[1] = kr;
+            p.out[2] = vr;
+            p.n_seg[0] = nq;
+            p.n_seg[1] = p.n_seg[2] = nkv;
+            p.cb_end[0] = nq / kSkinnyCols;
+            p.cb_end[1] = p.cb_end[0] + nkv / kSkinnyCols;
+            p.cb_end[2] = p.cb_end[1] + nkv / kSkinnyCols;
+            p.m = m;
+            p.k = k;
+            const int rc = lds_path(dev, m, k, 1, p.cb_end[2]) ? launch_skinny_lds<bf16_t, false>(st, 1, lds_params(p))
+                                                               : launch_skinny<bf16_t, false>(dev, st, 1, p, pws, pws_bytes);
+            if (rc) return rc;
+        } else {
+            const void* wts[3] = {q_proj_w, k_proj_w, v_proj_w};
+            void* os[3] = {qp, kr, vr};
+            const int ns[3] = {nq, nkv, nkv};
+            if (workspace && pws_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
+            for (int i = 0; i < 3; ++i)
+                if (lt_gemm(dev, st, 1, m, ns[i], k, normed, wts[i], os[i], workspace ? pws : nullptr) != 0)
+                    return SUPERSONIC_ERR_LAUNCH;
+        }
+        hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(m, Hq + Hkv), dim3(64), 0, st, qp, kr, vr, e);
+        if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
     }
     if (ev.after) (void)hipEventRecord(ev.after, st);
     return 0;

@@ -101,13 +101,18 @@ SIGNATURES = {
     "supersonic_attn_gfx950_qkv_proj_workspace_size": [_sz, _sz, _sz, _sz],
     "supersonic_attn_gfx950_qkv_proj":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz],
+    "supersonic_attn_gfx950_qkv_proj_rope_workspace_size": [_sz, _sz, _sz, _sz, _sz],
+    "supersonic_attn_gfx950_qkv_proj_rope":
+        [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+         _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p, _sz],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "supersonic_attn_gfx950_set_profile_events": [_p, _p],
     "supersonic_attn_rope_tables": [_sz, _sz, C.c_double, _p, _p],
     "supersonic_attn_version": [],
 }
 RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_gfx950_prefill_workspace_size": _sz,
-            "supersonic_attn_gfx950_o_proj_workspace_size": _sz, "supersonic_attn_gfx950_qkv_proj_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
+            "supersonic_attn_gfx950_o_proj_workspace_size": _sz, "supersonic_attn_gfx950_qkv_proj_workspace_size": _sz,
+            "supersonic_attn_gfx950_qkv_proj_rope_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
             "supersonic_attn_gfx950_set_profile_events": None}
 
 _LIB = None
@@ -396,6 +401,26 @@ def qkv_proj(ordinal, hidden, input_norm_w, q_proj_w, k_proj_w, v_proj_w, q_proj
         ordinal, _stream_ptr(stream), hd, rows, hid, nq, nkv, eps, _ptr(hidden), _ptr(input_norm_w),
         _ptr(q_proj_w), _ptr(k_proj_w), _ptr(v_proj_w), _ptr(q_proj_out), _ptr(k_out), _ptr(v_out),
         *_ws(workspace)))
+
+
+def qkv_proj_rope(ordinal, hidden, input_norm_w, q_proj_w, k_proj_w, v_proj_w, q_norm_w, k_norm_w, cos_table,
+                  sin_table, positions, q_out, gate_out, k_out, v_out, *, q_heads, kv_heads, head_dim, rotary_dim,
+                  eps=1e-6, qk_eps=1e-6, cache: Optional["KvCache"] = None, workspace=None, stream=None):
+    """``supersonic_attn_gfx950_qkv_proj_rope``: input norm + projections + QK norm + RoPE (+ cache append)."""
+    import torch
+    rows, hid = hidden.shape
+    hd = {torch.bfloat16: ScalarType.BF16, torch.float32: ScalarType.F32}[hidden.dtype]
+    desc = cache.desc() if cache is not None else None
+    _check("qkv_proj_rope", load().supersonic_attn_gfx950_qkv_proj_rope(
+        ordinal, _stream_ptr(stream), hd, rows, hid, q_heads, kv_heads, head_dim, rotary_dim, eps, qk_eps,
+        _ptr(hidden), _ptr(input_norm_w), _ptr(q_proj_w), _ptr(k_proj_w), _ptr(v_proj_w), _ptr(q_norm_w),
+        _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), _ptr(positions), _ptr(q_out), _ptr(gate_out),
+        _ptr(k_out), _ptr(v_out), None if desc is None else C.byref(desc), *_ws(workspace)))
+
+
+def qkv_proj_rope_workspace_size(rows, hidden_dim, q_heads, kv_heads, head_dim) -> int:
+    return int(load().supersonic_attn_gfx950_qkv_proj_rope_workspace_size(rows, hidden_dim, q_heads, kv_heads,
+                                                                         head_dim))
 
 
 def quantize_kv_fp8_ocp(ordinal, src, dst_fp8, dst_scale, num_kv_heads, seq_len, head_dim, max_t, pos_offset,

@@ -156,3 +156,20 @@ def test_rope_tables_validation(lib):
     assert lib.supersonic_attn_rope_tables(63, 4, 1e4, None, None) == K.ERR["ROTARY"]
     assert lib.supersonic_attn_rope_tables(64, 4, 0.0, None, None) == K.ERR["ROTARY"]
     assert lib.supersonic_attn_rope_tables(64, 4, 1e4, None, None) == K.ERR["NULL"]
+
+
+def test_qkv_proj_rope_validation(lib):
+    p = 0x1000  # never dereferenced: validation fails first
+    desc = K.KvCacheDesc()
+    f = lambda hd=2, hdim=256, hq=16, hkv=4, rot=64, x=p, cache=None: lib.supersonic_attn_gfx950_qkv_proj_rope(
+        0, None, hd, 4, 512, hq, hkv, hdim, rot, 1e-6, 1e-6, x, p, p, p, p, p, p, p, p, p, p, p, p, p,
+        cache, None, 0)
+    assert f(hd=0) == K.ERR["DTYPE"]
+    assert f(hdim=100) == K.ERR["HEAD_DIM"]
+    assert f(hkv=5) == K.ERR["HEADS"]
+    assert f(rot=63) == K.ERR["ROTARY"]
+    assert f(x=None) == K.ERR["NULL"]
+    desc.k = desc.v = p
+    desc.k_scale = desc.v_scale = p
+    assert f(cache=C.byref(desc)) == K.ERR["CACHE"]   # fp8 caches are not appended here
+    assert K.qkv_proj_rope_workspace_size(8, 4096, 16, 4, 256) > 8 * 4096 * 2

@@ -254,3 +254,95 @@ def test_decode_layer_chain():
     d = (h.float().cpu() - rh).abs()
     assert d.max().item() <= 2e-2 * max(1.0, rh.abs().max().item()) and d.mean().item() <= 2e-3, \
         f"chain: max {d.max().item():.3e} mean {d.mean().item():.3e}"
+
+
+def run_qkv_rope(hidden, nw, wq, wk, wv, qw, kw, cos, sin, pos, Hq, Hkv, D, rot, cache=None):
+    rows = hidden.shape[0]
+    mk = lambda n: torch.full((rows, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    q, gate, k, v = mk(Hq * D), mk(Hq * D), mk(Hkv * D), mk(Hkv * D)
+    K.qkv_proj_rope(0, hidden.to(DEV), nw.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), qw.to(DEV), kw.to(DEV),
+                    cos.to(DEV), sin.to(DEV), pos.to(DEV), q, gate, k, v, q_heads=Hq, kv_heads=Hkv, head_dim=D,
+                    rotary_dim=rot, cache=cache)
+    torch.cuda.synchronize()
+    return q.cpu(), gate.cpu(), k.cpu(), v.cpu()
+
+
+@pytest.mark.parametrize("rows,hid,Hq,Hkv,D,rot", [
+    (8, 4096, 16, 4, 256, 64),    # config-2 decode step: fused epilogue
+    (1, 2048, 8, 2, 256, 64),     # config-1 heads
+    (4, 1024, 8, 2, 128, 32),     # head_dim 128
+    (16, 4096, 16, 4, 256, 64),   # rows * hidden > 32768: projections, then the norm/RoPE kernel
+    (40, 1024, 8, 2, 256, 64),    # GEMM rows
+    (3, 512, 4, 2, 64, 16),       # head_dim 64
+])
+@pytest.mark.parametrize("with_cache", [False, True])
+def test_qkv_proj_rope_matches_oracle(rows, hid, Hq, Hkv, D, rot, with_cache):
+    """Input norm + Q/K/V projections + per-head QK RMSNorm + partial RoPE (+ KV append)
+    against the oracle's qkv_proj followed by prep_qk.  The projection may round a
+    value one bf16 ulp apart from the oracle (fp32 summation order), which the norm
+    and RoPE carry: q / k within 4 ulps of the result plus 2^-4 absolute (a rotated
+    pair can cancel, leaving a small result off by an ulp of its ~2-4 sized inputs),
+    v and gate within 2 ulps; at least 80% identical; the appended cache rows equal
+    the returned k / v bit for bit."""
+    announce(f"qkv_proj_rope rows={rows} hidden={hid} Hq={Hq} Hkv={Hkv} D={D} cache={with_cache}")
+    g = gen(88)
+    shape = O.LayerShape(Hq, Hkv, D, rot)
+    hidden = O.randn_bf16(g, rows, hid)
+    nw = O.randn_bf16(g, hid, std=0.1)
+    wq, wk, wv = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (Hq * 2 * D, Hkv * D, Hkv * D))
+    qw, kw = O.norm_weights(g, D)
+    cos, sin = O.rope_tables(rot, 5000, 1.0e7)
+    pos = torch.randint(0, 4999, (rows,), generator=g).to(torch.int32)
+    cache = None
+    if with_cache:
+        cache = K.KvCache(torch.zeros(rows, Hkv, 5000, D, dtype=torch.bfloat16, device=DEV),
+                          torch.zeros(rows, Hkv, 5000, D, dtype=torch.bfloat16, device=DEV))
+    q, gate, k, v = run_qkv_rope(hidden, nw, wq, wk, wv, qw, kw, cos, sin, pos, Hq, Hkv, D, rot, cache)
+    rq, rk, rv = O.qkv_proj(hidden, nw, wq, wk, wv)
+    oq, og, ok = O.prep_qk(shape, rq, rk, qw, kw, cos, sin, pos.long())
+    for name, out, ref, n_ulp, floor in (("q", q, oq.reshape(rows, -1), 4, 2.0 ** -4),
+                                         ("k", k, ok.reshape(rows, -1), 4, 2.0 ** -4),
+                                         ("gate", gate, og.reshape(rows, -1), 2, 2.0 ** -9), ("v", v, rv, 2, 2.0 ** -9)):
+        assert_ulps(out, ref, n_ulp * ulp(ref) + floor, f"qkv_rope {name}")
+        assert (out.float() == ref).float().mean().item() > 0.8, name
+    if with_cache:
+        for r in range(rows):
+            p = int(pos[r])
+            assert torch.equal(cache.k[r, :, p].cpu(), k[r].reshape(Hkv, D))
+            assert torch.equal(cache.v[r, :, p].cpu(), v[r].reshape(Hkv, D))
+
+
+def test_decode_layer_chain_fused_projection():
+    """qkv_proj_rope (with the KV append) -> decode_attend (gate) -> o_proj + residual
+    against the oracle's decode-layer chain (config-2 heads, hidden 4096, B = 4)."""
+    announce("decode layer chain, fused projection")
+    g = gen(89)
+    B, Hq, Hkv, D, rot, hid, L = 4, 16, 4, 256, 64, 4096, 700
+    shape = O.LayerShape(Hq, Hkv, D, rot)
+    hidden = O.randn_bf16(g, B, hid)
+    nw = O.randn_bf16(g, hid, std=0.1)
+    wq, wk, wv = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (Hq * 2 * D, Hkv * D, Hkv * D))
+    wo = O.randn_bf16(g, hid, Hq * D, std=(Hq * D) ** -0.5)
+    qw, kw = O.norm_weights(g, D)
+    cos, sin = O.rope_tables(rot, L + 2, 1.0e7)
+    kc = O.randn_bf16(g, B, Hkv, L + 1, D)
+    vc = O.randn_bf16(g, B, Hkv, L + 1, D)
+    pos = torch.tensor([L, L - 9, 250, 0], dtype=torch.int32)
+    cache = K.KvCache(kc.to(DEV), vc.to(DEV))
+    q, gate, _, _ = (t.to(DEV) for t in run_qkv_rope(hidden, nw, wq, wk, wv, qw, kw, cos, sin, pos, Hq, Hkv, D, rot,
+                                                      cache))
+    attn = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    K.decode_attend(0, q.reshape(B, Hq, D), (pos + 1).to(DEV), cache, attn, q_heads=Hq, kv_heads=Hkv, head_dim=D,
+                    max_kv_len=L + 1, gate=gate)
+    h = hidden.to(DEV)
+    K.o_proj_residual(0, attn, wo.to(DEV), h)
+    torch.cuda.synchronize()
+    rq, rk, rv = O.qkv_proj(hidden, nw, wq, wk, wv)
+    ra = O.decode_layer(shape, rq, rk, rv, qw, kw, cos, sin, pos.tolist(), [kc[b].clone() for b in range(B)],
+                        [vc[b].clone() for b in range(B)])
+    check_a = (attn.float().cpu() - ra).abs()
+    assert check_a.max().item() <= 2e-2 and check_a.mean().item() <= 2e-3, f"attn {check_a.max().item():.3e}"
+    rh = O.o_proj_residual(ra, wo, hidden)
+    d = (h.float().cpu() - rh).abs()
+    assert d.max().item() <= 2e-2 * max(1.0, rh.abs().max().item()) and d.mean().item() <= 2e-3, \
+        f"chain: max {d.max().item():.3e} mean {d.mean().item():.3e}"
