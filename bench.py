@@ -499,11 +499,20 @@ class Workloads:
             with torch.cuda.graph(graph, stream=st):
                 layer()
             graph_ms = timed_on_stream(graph.replay)
+            # the same layer as one persistent kernel
+            lws = torch.zeros(K.decode_layer_workspace_size(B, hid, Hq, Hkv, D, L + 1), dtype=torch.uint8,
+                              device=self.dev)
+
+            def persistent():
+                K.decode_layer(0, hidden, nw, wq, wk, wv, qw, kw, wo, cos, sin, pos, cache, lws, q_heads=Hq,
+                               kv_heads=Hkv, head_dim=D, rotary_dim=rot, max_kv_len=L + 1, stream=st)
+            pers_ms = timed_on_stream(persistent)
             res[name] = {"eager_us_per_layer": round(eager_ms * 1e3, 2), "graph_us_per_layer": round(graph_ms * 1e3, 2),
-                         "launches_per_layer": 4}
+                         "persistent_us_per_layer": round(pers_ms * 1e3, 2), "launches_per_layer": 4}
             del kc, vc, cache, graph
             torch.cuda.empty_cache()
-        return {"workload": "decode layer (qkv_proj + fused decode + o_proj), eager vs HIP graph", **res}
+        return {"workload": "decode layer (input norm + Q/K/V projections, fused decode, o_proj + residual): eager "
+                            "launches vs HIP graph replay vs the persistent one-kernel layer", **res}
 
     def copy(self):
         """Plain device copy of known size, to calibrate FETCH_SIZE/WRITE_SIZE counters."""

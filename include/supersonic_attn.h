@@ -318,6 +318,37 @@ int supersonic_attn_gfx950_qkv_proj_rope(
     const void* sin_table, const int32_t* positions, void* q_out, void* gate_out, void* k_out,
     void* v_out, const supersonic_kv_cache* cache, void* workspace, size_t workspace_bytes);
 
+/* One whole attention layer of a decode step in a single persistent kernel
+ * (the attention phase as a device function between the projections, as the
+ * reference's persistent megakernel runs it: qwen36_moe_persistent/
+ * full_attn_phase.cuh:1-20, full_attention_4b.hip:4842-5577):
+ *   normed = RMSNorm(hidden) (1 + input_norm_w, eps)
+ *   q_proj, k, v = normed . W_q^T, W_k^T, W_v^T               (bf16)
+ *   attn = supersonic_attn_gfx950_decode(q_proj, k, v, ...)  (QK norm with
+ *          qk_eps, RoPE, KV append at positions[b], attention, gate)
+ *   hidden = bf16(hidden + bf16(attn . W_o^T))                (in place)
+ * hidden [batch, hidden_dim] bf16 (hidden_dtype 2) or f32 holding bf16 values
+ * (1); weights as supersonic_attn_gfx950_qkv_proj / _o_proj_residual; cache,
+ * positions, tables as supersonic_attn_gfx950_decode.  One workgroup per
+ * compute unit, three phases separated by device-wide barriers (every
+ * workgroup of the grid is resident at once).  Limits: batch <= 16,
+ * batch * hidden_dim <= 32768 and batch * q_heads * head_dim <= 32768,
+ * hidden_dim % 16 == 0, head_dim 128/256, q_heads / kv_heads <= 4, 16-byte
+ * aligned hidden and weights (otherwise SUPERSONIC_ERR_RANGE: use the
+ * separate entry points).  workspace (required): at least
+ * supersonic_attn_gfx950_decode_layer_workspace_size() bytes, zero-filled
+ * before its first use (barrier and split counters that every call leaves at
+ * zero); calls sharing it must not overlap.  Asynchronous on `stream`. */
+size_t supersonic_attn_gfx950_decode_layer_workspace_size(
+    size_t batch, size_t hidden_dim, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len);
+int supersonic_attn_gfx950_decode_layer(
+    size_t device_ordinal, void* stream, int hidden_dtype, int kv_dtype, size_t batch, size_t hidden_dim,
+    size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim, size_t max_kv_len, float eps,
+    float qk_eps, float scale, void* hidden, const void* input_norm_w, const void* q_proj_w,
+    const void* k_proj_w, const void* v_proj_w, const void* q_norm_w, const void* k_norm_w,
+    const void* o_proj_w, const void* cos_table, const void* sin_table, const int32_t* positions,
+    const supersonic_kv_cache* cache, void* workspace, size_t workspace_bytes);
+
 /* Output projection with the residual add, after the gated attention:
  *   hidden[r, j] = bf16(hidden[r, j] + bf16(sum_c attn[r, c] * o_proj_w[j, c]))
  * attn [rows, attn_dim] bf16 (the fused decode/prefill `out`), o_proj_w

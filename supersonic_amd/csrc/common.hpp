@@ -155,6 +155,39 @@ __device__ __forceinline__ float load_agent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Device-coherent accesses of data another workgroup of the same kernel wrote
+// (agent-scope relaxed atomics: sc1 loads and write-through stores).
+__device__ __forceinline__ uint16_t load_agent_u16(const uint16_t* p) {
+    return __hip_atomic_load(const_cast<uint16_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent_u16(uint16_t* p, uint16_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u32x4_v ld16_agent(const void* p) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<void*>(p));
+    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return u32x4_v{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b),
+                   static_cast<uint32_t>(b >> 32)};
+}
+// store_f32 through the coherent path (bf16 / f16 / f32 elements)
+template <typename T> __device__ __forceinline__ void store_f32_agent(T* p, size_t i, float x);
+template <> __device__ __forceinline__ void store_f32_agent<float>(float* p, size_t i, float x) { store_agent(p + i, x); }
+template <> __device__ __forceinline__ void store_f32_agent<bf16_t>(bf16_t* p, size_t i, float x) {
+    store_agent_u16(reinterpret_cast<uint16_t*>(p) + i, static_cast<uint16_t>(f32_to_bf16_bits(x)));
+}
+template <> __device__ __forceinline__ void store_f32_agent<f16_t>(f16_t* p, size_t i, float x) {
+    store_agent_u16(reinterpret_cast<uint16_t*>(p) + i, static_cast<uint16_t>(f32_to_f16_bits(x)));
+}
+
+// Element seg (0..2) of a 3-entry parameter array by selects: indexing a kernel
+// parameter's array with a run-time index would copy the parameters to
+// private (scratch) memory.
+template <typename T>
+__device__ __forceinline__ T pick3(const T (&a)[3], int seg) {
+    return seg == 0 ? a[0] : (seg == 1 ? a[1] : a[2]);
+}
+
 // Workgroup barrier that waits only for LDS traffic: unlike __syncthreads it
 // leaves outstanding global loads in flight.
 __device__ __forceinline__ void lds_barrier() {

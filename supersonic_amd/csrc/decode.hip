@@ -43,766 +43,14 @@
 #include "common.hpp"
 #include "kv_view.hpp"
 
+#include "decode_split.hpp"
+
 namespace ssa {
-
-struct DecodeParams {
-    KvView kv;
-    const uint16_t* q;        // attend: q [B, Hq, D]; fused: q_proj [B, Hq*2D]
-    int64_t q_bstride;        // elements between batch rows of q
-    int64_t q_hstride;        // elements between heads of q
-    const int32_t* lens;      // kv_lens [B] (attend) or positions [B] (fused)
-    int len_plus;             // 0 (attend) or 1 (fused: len = position + 1)
-    int Hq, Hkv, G, chunk, nsplit;
-    // Ragged plan (ragged != 0): the workgroups of a 1-D grid split the batch's
-    // total length into chunks of about total * Hkv / target tokens, so every
-    // workgroup gets about the same number of tokens whatever the lengths;
-    // chunk and nsplit are then unused.
-    int ragged, B, target, min_chunk;
-    float scale_log2;         // softmax scale * log2(e)
-    int fused;
-    const uint16_t* k_new;    // [B, Hkv*D] bf16
-    const uint16_t* v_new;
-    const uint16_t* q_norm_w; // [D] bf16
-    const uint16_t* k_norm_w;
-    const uint16_t* cos_t;    // [max_pos, half_rot] bf16
-    const uint16_t* sin_t;
-    int half_rot;
-    float eps;
-    float* part_o;            // [rows, D], row of (b, h, split) = pre_b * Hq + h * n_b + split
-    float* part_ml;           // [rows, 2] (max in log2 units, sum)
-    unsigned* arrivals;       // [B, Hkv] split arrival counters, zero between calls
-    const uint16_t* gate;     // NULL, or gate element (b, h, d) at b*g_bstride + h*g_hstride + d
-    int64_t g_bstride, g_hstride;
-    void* out;                // [B, Hq*D] of QT
-};
-
-template <typename QT> struct Mfma;
-template <> struct Mfma<bf16_t> {
-    typedef bf16x8_v op;
-    static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-};
-template <> struct Mfma<f16_t> {
-    typedef f16x8_v op;
-    static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-};
-
-template <typename OP>
-__device__ __forceinline__ OP as_op(const u32x4_v& w) {
-    OP r;
-    __builtin_memcpy(&r, &w, 16);
-    return r;
-}
-
-// 8 e4m3 bytes -> 8 bf16 (exact: every e4m3 value is a bf16 value), two
-// bytes per gfx950 v_cvt_scalef32_pk_bf16_fp8 at scale 1.
-__device__ __forceinline__ u32x4_v fp8x8_to_bf16x8(u32x2_v w) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    u32x4_v r;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        r[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, false));
-        r[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, true));
-    }
-    return r;
-}
-
-// First of the 8 consecutive dims that lane group g (= lane >> 4) holds in
-// QK^T k-step s, for Q (A operand) and K (B operand) alike: 32 s + 8 g for
-// 16-bit K; for e4m3 K a lane loads 16 dims (16 bytes) at once, so k-steps
-// 2 ss and 2 ss + 1 take the two halves: 64 ss + 16 g + 8 (s & 1).
-template <bool FP8>
-__device__ __forceinline__ constexpr int kdim(int s, int g) {
-    return FP8 ? 64 * (s >> 1) + 16 * g + 8 * (s & 1) : 32 * s + 8 * g;
-}
-
-__device__ __forceinline__ void fp8x8_to_f32(u32x2_v w, float* f) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        f32x2_v lo = fp8x2_to_f32(w[i], false);
-        f32x2_v hi = fp8x2_to_f32(w[i], true);
-        f[4 * i + 0] = lo[0];
-        f[4 * i + 1] = lo[1];
-        f[4 * i + 2] = hi[0];
-        f[4 * i + 3] = hi[1];
-    }
-}
-
-// Buffer resource for a base that is uniform across the wave (forced into
-// SGPRs: it can come from a block-table load the compiler cannot prove
-// uniform).  Reads at or past `bytes` return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const uint8_t* base, int bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
-    void* u = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(u, static_cast<short>(0), bytes, 0x00020000);
-}
-
-template <typename QT>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return Elem<QT>::from_f32(a) | (Elem<QT>::from_f32(b) << 16);
-}
-
-// Waves per workgroup: 8 for head groups up to 4 (one workgroup per CU, two
-// waves per SIMD at up to 256 registers); the larger groups need more
-// registers and run 4 (two workgroups per CU for 8, one for 16).
-__host__ __device__ constexpr int decode_waves(int GP) { return GP <= 4 ? 8 : 4; }
 
 template <typename QT, bool FP8, int D, int GP>
 __global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(DecodeParams p) {
-    static_assert(D % 64 == 0 && D <= 512, "head_dim");
-    static_assert(GP == 4 || GP == 8 || GP == 16, "padded group");
-    typedef typename Mfma<QT>::op op_t;
-    constexpr int KSTEPS = D / 32;
-    constexpr int LPT = D / 8;       // lanes per token row in the V layout
-    constexpr int TPI = 64 / LPT;    // tokens per V load instruction
-    constexpr int VINS = 16 / TPI;   // V load instructions per 16-token block
-    constexpr int ESZ = FP8 ? 1 : 2;
-
-    constexpr int NW = decode_waves(GP);
-    constexpr int NT = 64 * NW;
-    __shared__ float smem[NW * GP * D];        // q staging, then the wave merge
-    __shared__ float p_s[NW][16][GP];          // per-wave probabilities
-    __shared__ float kn_s[D], vn_s[D];         // the new token (fused owner split)
-    __shared__ float ml_s[NW][GP][2];
-    __shared__ int next_blk;                   // next 16-token block to claim
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Work item (b, kv head, split), chunk length, and the partial rows of
-    // sequence b: pre_b splits before it, n_b of its own per head.
-    int split, kvh, b, chunk, n_b;
-    int64_t pre_b;
-    if (p.ragged) {
-        // Every workgroup plans the same way from the lengths: chunk =
-        // ceil(total * Hkv / target) rounded up to 16 (at least min_chunk),
-        // sequence b gets n_b = max(1, ceil(len_b / chunk)) splits per kv
-        // head, each of them ceil(len_b / n_b) tokens (rounded up to 16), items
-        // are ordered (b, kv head, split), and workgroup i takes item i (past
-        // the last item it has nothing to do).
-        __shared__ int plan_s[6];
-        if (wave == 0) {
-            int64_t tot = 0;
-            for (int b0 = 0; b0 < p.B; b0 += 64) {
-                const int bi = b0 + lane;
-                tot += bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
-            }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) tot += __shfl_xor(tot, o);
-            // Per-sequence rounding can push the item count past the target
-            // (a second, mostly idle round): grow the chunk in proportion
-            // until the items fit (a few passes; uniform lengths need none).
-            int64_t c = (tot * p.Hkv + p.target - 1) / p.target;
-            c = max((c + 15) / 16 * 16, static_cast<int64_t>(p.min_chunk));
-            for (int pass = 0; pass < 4; ++pass) {
-                int64_t items = 0;
-                for (int b0 = 0; b0 < p.B; b0 += 64) {
-                    const int bi = b0 + lane;
-                    const int64_t l = bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
-                    items += bi < p.B ? max(static_cast<int64_t>(1), (l + c - 1) / c) : 0;
-                }
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) items += __shfl_xor(items, o);
-                items *= p.Hkv;
-                if (items <= p.target) break;
-                c = (c * items + p.target - 1) / p.target;
-                c = (c + 15) / 16 * 16;
-            }
-            const int ch = static_cast<int>(c);
-            if (lane == 0) plan_s[0] = -1;
-            const int w = blockIdx.x;
-            int run = 0, run_n = 0;  // items and splits of the sequences before b0
-            for (int b0 = 0; b0 < p.B; b0 += 64) {
-                const int bi = b0 + lane;
-                const int l = bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
-                const int n = bi < p.B ? max(1, (l + ch - 1) / ch) : 0;
-                int incl = n;        // inclusive scan of the split counts
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const int t = __shfl_up(incl, o);
-                    if (lane >= o) incl += t;
-                }
-                const int first = run + (incl - n) * p.Hkv;  // first item of sequence bi
-                if (bi < p.B && w >= first && w < first + n * p.Hkv) {
-                    plan_s[0] = bi;
-                    plan_s[1] = (w - first) / n;
-                    plan_s[2] = (w - first) % n;
-                    plan_s[3] = n;
-                    plan_s[4] = run_n + incl - n;
-                    // the sequence's n splits share its length equally (16-token
-                    // blocks), so no split is left with a short remainder
-                    plan_s[5] = l > 0 ? ((l + n - 1) / n + 15) / 16 * 16 : ch;
-                }
-                const int tot_n = __shfl(incl, 63);
-                run += tot_n * p.Hkv;
-                run_n += tot_n;
-            }
-        }
-        __syncthreads();
-        b = plan_s[0];
-        if (b < 0) return;  // uniform
-        kvh = plan_s[1];
-        split = plan_s[2];
-        n_b = plan_s[3];
-        pre_b = plan_s[4];
-        chunk = plan_s[5];
-    } else {
-        split = blockIdx.x;
-        kvh = blockIdx.y;
-        b = blockIdx.z;
-        chunk = p.chunk;
-        n_b = p.nsplit;
-        pre_b = static_cast<int64_t>(b) * p.nsplit;
-    }
-    const int len = p.lens[b] + p.len_plus;
-    const int t_begin = split * chunk;
-    if (t_begin >= len) {  // uniform: ragged batch, nothing to do
-        if (len <= 0 && split == 0) {
-            // No tokens at all: the output is zero (what the merge of no splits gives).
-            for (int idx = tid; idx < p.G * D; idx += NT) {
-                const int h = kvh * p.G + idx / D;
-                store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + idx % D, 0.f);
-            }
-        }
-        return;
-    }
-    const int t_end = min(len, t_begin + chunk);
-    const int G = p.G;
-    const int pos = len - 1;
-    const bool owner = p.fused && pos >= t_begin && pos < t_end;
-
-    const int n_s = lane & 15;           // score lane: token within the block
-    const int vt = lane / LPT;           // V lane: token within the instruction
-    const int vd = (lane % LPT) * 8;     // V lane: first dim
-    // Cached tokens of this split; the owner's new token (the last one) is
-    // handled after the loop.
-    const int t_main = owner ? pos : t_end;
-    const int nblk = (t_main - t_begin + 15) >> 4;
-    const uint8_t* kbase = p.kv.k;
-    const uint8_t* vbase = p.kv.v;
-
-    // Block data of one 16-token block, loaded one block ahead (registers).
-    struct Blk {
-        op_t kb[FP8 ? 1 : KSTEPS];
-        u32x4_v kr8[FP8 ? KSTEPS / 2 : 1];  // raw e4m3 K, 16 dims a load: converted when the block is processed
-        u32x4_v vr16[FP8 ? 1 : VINS];
-        u32x2_v vr8[FP8 ? VINS : 1];
-        float ksc, vsc;
-    };
-    // Buffer resources bound to the block's live rows (a block lies inside one
-    // page): rows past kv_len read as zeros, so every load is one per-lane
-    // offset plus a constant, with no per-load clamping.
-    const int k_lane_off = n_s * D * ESZ + kdim<FP8>(0, lane >> 4) * ESZ;
-    // Cache policy of the K/V loads: nontemporal for the bf16 8-wave kernel
-    // (every byte is read once; 6.0 -> 7.1 TB/s for its access pattern on
-    // MI355X); the FP8 and 4-wave variants measured faster without it.
-    constexpr int kStream = (!FP8 && NW == 8) ? 2 : 0;
-    const int v_lane_off = (vt * D + vd) * ESZ;
-    auto fetch = [&](int blk, Blk& B) {
-        const int t0 = t_begin + blk * 16;
-        // The page comes through the scalar cache (lgkmcnt): waiting for it
-        // does not wait for the other block's vector loads still in flight.
-        const int ub = __builtin_amdgcn_readfirstlane(b), uk = __builtin_amdgcn_readfirstlane(kvh);
-        const int ut = __builtin_amdgcn_readfirstlane(t0);
-        const int64_t base = p.kv.row_uniform(ub, uk, ut, D);
-        const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(16, t_main - t0)));  // wave-uniform
-        const __amdgpu_buffer_rsrc_t kr = uniform_rsrc(kbase + base * ESZ, nvalid * D * ESZ);
-        const __amdgpu_buffer_rsrc_t vr = uniform_rsrc(vbase + base * ESZ, nvalid * D * ESZ);
-        // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
-        if constexpr (!FP8) {
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s)
-                B.kb[s] = as_op<op_t>(__builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * s, 0, kStream)));
-        } else {
-            // raw bytes only, 16 per lane: converted when the block is processed
-#pragma unroll
-            for (int ss = 0; ss < KSTEPS / 2; ++ss)
-                B.kr8[ss] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * ss, 0, kStream));
-        }
-        // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
-#pragma unroll
-        for (int j = 0; j < VINS; ++j) {
-            const int jo = TPI * j * D * ESZ;
-            if constexpr (!FP8) B.vr16[j] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane_off, jo, kStream));
-            else B.vr8[j] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane_off, jo, kStream));
-        }
-        B.ksc = 1.f;
-        B.vsc = 1.f;
-        if constexpr (FP8) {
-            const int64_t sb = p.kv.srow_uniform(ub, uk, ut);
-            const int kn = max(0, min(n_s, nvalid - 1));  // nvalid is 0 when a split holds only the new token
-            B.ksc = p.kv.ks[sb + kn];
-            B.vsc = p.kv.vs[sb + kn];
-        }
-    };
-
-    Blk A, Bn;  // the block register sets (A's first fetch is issued in the prologue)
-    // ---------------------------------------------------------------- prologue
-    if (tid == 0) next_blk = NW;  // blocks 0 .. NW-1 are the waves' first
-    // One wave per row: rows 0 .. G-1 are the q heads, row G (owner split of
-    // the fused step) is the new k (with v alongside).  Lane l holds dims
-    // l + 64 k.  All global loads of a row go out before any arithmetic, so the
-    // prologue costs one memory round trip.
-    {
-        constexpr int EPL = D / 64;
-        const int hr = p.fused ? p.half_rot : 0;
-        const int rows = G + (owner ? 1 : 0);
-        // A row's global loads (q head, or the new k with v), clamped to a real
-        // row so they need no branch.
-        auto row_loads = [&](const int r, float (&x)[EPL], float (&vx)[EPL], float (&w)[EPL], float (&cs)[EPL],
-                             float (&sn)[EPL]) {
-            // Branch-free: every pointer is chosen per wave (an absent input is
-            // replaced by the row itself, a valid address whose value is then
-            // ignored) and every index is clamped, so the row's loads go out
-            // back to back and one wait covers them all.
-            const bool is_k = r == G;
-            const uint16_t* qrow = reinterpret_cast<const uint16_t*>(p.q) + b * p.q_bstride +
-                                   static_cast<int64_t>(kvh * G + min(r, G - 1)) * p.q_hstride;
-            const int64_t ko = (static_cast<int64_t>(b) * p.Hkv + kvh) * D;
-            const uint16_t* xsrc = is_k ? p.k_new + ko : qrow;
-            const uint16_t* vsrc = is_k ? p.v_new + ko : qrow;
-            const uint16_t* wsrc = p.fused ? (is_k ? p.k_norm_w : p.q_norm_w) : qrow;
-            const uint16_t* ctab = hr > 0 ? p.cos_t + static_cast<int64_t>(pos) * hr : qrow;
-            const uint16_t* stab = hr > 0 ? p.sin_t + static_cast<int64_t>(pos) * hr : qrow;
-            uint32_t xr[EPL], vr[EPL], wr[EPL], cr[EPL], sr[EPL];
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) {
-                const int d = lane + 64 * k;
-                const int ti = d < hr ? d : (d < 2 * hr ? d - hr : 0);
-                xr[k] = xsrc[d];
-                vr[k] = vsrc[d];
-                wr[k] = wsrc[d];
-                cr[k] = ctab[ti];
-                sr[k] = stab[ti];
-            }
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) {
-                const int d = lane + 64 * k;
-                x[k] = is_k ? bf16_bits_to_f32(xr[k]) : Elem<QT>::to_f32(xr[k]);
-                vx[k] = bf16_bits_to_f32(vr[k]);
-                w[k] = bf16_bits_to_f32(wr[k]);
-                const bool rot = d < 2 * hr;
-                cs[k] = rot ? bf16_bits_to_f32(cr[k]) : 0.f;
-                sn[k] = rot ? bf16_bits_to_f32(sr[k]) : 0.f;
-            }
-        };
-        auto row_compute = [&](const int r, float (&x)[EPL], float (&vx)[EPL], float (&w)[EPL], float (&cs)[EPL],
-                               float (&sn)[EPL]) {
-            const bool is_k = r == G;
-            float* row = is_k ? kn_s : &smem[r * D];
-            if (p.fused) {
-                // Per-head RMSNorm with (1 + w), bf16 result (full_attention_4b.hip:5142-5191).
-                float ss = 0.f;
-#pragma unroll
-                for (int k = 0; k < EPL; ++k) ss += x[k] * x[k];
-                ss = wave_sum(ss);
-                const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
-#pragma unroll
-                for (int k = 0; k < EPL; ++k) x[k] = bf16_round(x[k] * inv * (w[k] + 1.0f));
-                // Rotate-half partial RoPE at the new token's position (:5193-5224);
-                // the partner of dim d < 2 hr is d +- hr, read from the row in LDS.
-                if (hr > 0) {
-#pragma unroll
-                    for (int k = 0; k < EPL; ++k) row[lane + 64 * k] = x[k];
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-                    for (int k = 0; k < EPL; ++k) {
-                        const int d = lane + 64 * k;
-                        if (d < 2 * hr) {
-                            const float other = row[d < hr ? d + hr : d - hr];
-                            x[k] = d < hr ? bf16_round(x[k] * cs[k] - other * sn[k])
-                                          : bf16_round(other * sn[k] + x[k] * cs[k]);
-                        }
-                    }
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) {
-                row[lane + 64 * k] = x[k];
-                if (is_k) vn_s[lane + 64 * k] = vx[k];
-            }
-        };
-        // This wave's first row goes out first, then the wave's first K/V
-        // block: waiting for the row (vmcnt drains in issue order) does not
-        // wait for the block, whose round trip overlaps the norm and RoPE.
-        {
-            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
-            row_loads(min(wave, rows - 1), x, vx, w, cs, sn);
-            fetch(max(0, min(wave, nblk - 1)), A);
-            if (wave < rows) row_compute(wave, x, vx, w, cs, sn);
-        }
-        for (int r = wave + NW; r < rows; r += NW) {
-            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
-            row_loads(r, x, vx, w, cs, sn);
-            row_compute(r, x, vx, w, cs, sn);
-        }
-        // heads G .. GP-1 are zero rows of the padded MFMA operand
-        for (int idx = G * D + tid; idx < GP * D; idx += NT) smem[idx] = 0.f;
-    }
-    lds_barrier();
-    if (p.fused && owner) {
-        // KV append at slot pos (:5226-5296); FP8 uses the absmax scale and OCP e4m3.
-        // uniform indices: the table entry comes through the scalar cache and
-        // the wait for it leaves the first K/V block's loads in flight
-        const int ub = __builtin_amdgcn_readfirstlane(b), uk = __builtin_amdgcn_readfirstlane(kvh);
-        const int up = __builtin_amdgcn_readfirstlane(pos);
-        const int64_t off = p.kv.row_uniform(ub, uk, up, D);
-        if constexpr (!FP8) {
-            uint16_t* kc = reinterpret_cast<uint16_t*>(p.kv.k) + off;
-            uint16_t* vc = reinterpret_cast<uint16_t*>(p.kv.v) + off;
-            for (int d = tid; d < D; d += NT) {
-                kc[d] = static_cast<uint16_t>(f32_to_bf16_bits(kn_s[d]));
-                vc[d] = static_cast<uint16_t>(f32_to_bf16_bits(vn_s[d]));
-            }
-        } else {
-            if (wave < 2) {
-                const float* src = wave == 0 ? kn_s : vn_s;
-                uint8_t* dst = (wave == 0 ? p.kv.k : p.kv.v) + off;
-                float am = 0.f;
-                for (int d = lane; d < D; d += 64) am = fmaxf(am, fabsf(src[d]));
-                am = wave_max(am);
-                const float sc = fmaxf(am / 448.0f, 1e-12f);
-                const float inv = 1.0f / sc;
-                for (int d = lane * 4; d < D; d += 256) {
-                    const uint32_t c4 = f32x4_to_fp8x4(src[d] * inv, src[d + 1] * inv,
-                                                       src[d + 2] * inv, src[d + 3] * inv);
-                    *reinterpret_cast<uint32_t*>(dst + d) = c4;
-                }
-                if (lane == 0) (wave == 0 ? p.kv.ks : p.kv.vs)[p.kv.srow_uniform(ub, uk, up)] = sc;
-            }
-        }
-    }
-
-    // Q as the MFMA A operand: row = head (lane & 15), k = dims 32s + 8(lane>>4) + j.
-    // Kept in LDS (one copy for the 4 waves) and read back per block, which
-    // leaves registers for the next block's loads.
-    __shared__ u32x4_v qop_s[KSTEPS * 64];
-    if (wave == 0) {
-        const int hh = lane & 15;
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            u32x4_v w;
-            const int dk = kdim<FP8>(s, lane >> 4);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // clamped read and a select: a branch here would make the
-                // compiler wait for the wave's outstanding K/V loads
-                const int hc = min(hh, G - 1);
-                const float a = smem[hc * D + dk + 2 * j];
-                const float c = smem[hc * D + dk + 2 * j + 1];
-                w[j] = hh < G ? pack2<QT>(a, c) : 0u;
-            }
-            qop_s[s * 64 + lane] = w;
-        }
-    }
-    lds_barrier();  // smem is reused by the merge below
-
-    // ---------------------------------------------------------------- main loop
-    float m[4], lsum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m[i] = -1e30f; lsum[i] = 0.f; }
-    float acc[GP][8];
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-
-    // One 16-token block: scores on the MFMA pipe, online softmax per head,
-    // PV on VALU.  Tokens n_s >= nv are masked.  vdec(j, vf) yields the 8
-    // dims of V row TPI*j + vt as floats.
-    auto process = [&](int nv, const op_t (&kb)[KSTEPS], float ksc, float vsc, auto&& vdec) {
-        f32x4_v sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) sc = Mfma<QT>::mma(as_op<op_t>(qop_s[s * 64 + lane]), kb[s], sc);
-
-        const bool valid = n_s < nv;
-        float pr[4], al[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float s2 = valid ? sc[i] * (p.scale_log2 * ksc) : -INFINITY;
-            const float bm = row16_max(s2);
-            const float mn = fmaxf(m[i], bm);
-            al[i] = __builtin_amdgcn_exp2f(m[i] - mn);
-            const float pe = __builtin_amdgcn_exp2f(s2 - mn);
-            lsum[i] = lsum[i] * al[i] + pe;
-            m[i] = mn;
-            pr[i] = pe * vsc;
-        }
-        if (4 * (lane >> 4) < GP) {
-            f32x4_v pv = {pr[0], pr[1], pr[2], pr[3]};
-            *reinterpret_cast<f32x4_v*>(&p_s[wave][n_s][4 * (lane >> 4)]) = pv;
-        }
-        float alpha[GP];
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-            alpha[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[h & 3]), 16 * (h >> 2)));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // Rescale only when some head's running max moved (alpha != 1; the
-        // factors are wave-uniform, so this is a scalar branch): after the
-        // first blocks the max rarely changes.
-        bool moved = false;
-#pragma unroll
-        for (int h = 0; h < GP; ++h) moved |= alpha[h] != 1.0f;
-        if (moved) {
-#pragma unroll
-            for (int h = 0; h < GP; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
-        }
-
-#pragma unroll
-        for (int j = 0; j < VINS; ++j) {
-            const int tn = TPI * j + vt;
-            float vf[8];
-            vdec(j, vf);
-            float pv[GP];
-#pragma unroll
-            for (int h4 = 0; h4 < GP / 4; ++h4) {
-                const f32x4_v t = *reinterpret_cast<const f32x4_v*>(&p_s[wave][tn][4 * h4]);
-                pv[4 * h4] = t[0];
-                pv[4 * h4 + 1] = t[1];
-                pv[4 * h4 + 2] = t[2];
-                pv[4 * h4 + 3] = t[3];
-            }
-#pragma unroll
-            for (int h = 0; h < GP; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pv[h], vf[e], acc[h][e]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-    };
-    auto process_blk = [&](int blk, Blk& B) {
-        const int t0 = t_begin + blk * 16;
-        auto vdec = [&](int j, float (&vf)[8]) {
-            if constexpr (!FP8) unpack8<QT>(B.vr16[j], vf);
-            else fp8x8_to_f32(B.vr8[j], vf);
-        };
-        if constexpr (!FP8) {
-            process(min(16, t_main - t0), B.kb, B.ksc, B.vsc, vdec);
-        } else {
-            op_t kb[KSTEPS];
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) {
-                const u32x4_v& w = B.kr8[s >> 1];
-                kb[s] = as_op<op_t>(fp8x8_to_bf16x8((s & 1) ? u32x2_v{w[2], w[3]} : u32x2_v{w[0], w[1]}));
-            }
-            process(min(16, t_main - t0), kb, B.ksc, B.vsc, vdec);
-        }
-    };
-
-    // Software pipeline: the next block's loads are in flight while the
-    // current block is computed (two register sets, unrolled by two).
-    // Blocks are claimed from an LDS counter (wave w starts with block w), so
-    // a wave whose loads are served more slowly simply takes fewer blocks and
-    // the waves of the workgroup finish together.
-    auto take = [&]() {
-        int v = 0;
-        if (lane == 0) v = atomicAdd(&next_blk, 1);
-        return __builtin_amdgcn_readfirstlane(v);
-    };
-    {
-        int c0 = wave, c1 = nblk;
-        if (c0 < nblk) {
-            c1 = take();
-            if (c1 < nblk) fetch(c1, Bn);
-        }
-        while (c0 < nblk) {
-            process_blk(c0, A);
-            if (c1 >= nblk) break;
-            c0 = take();
-            if (c0 < nblk) fetch(c0, A);
-            process_blk(c1, Bn);
-            if (c0 >= nblk) break;
-            c1 = take();
-            if (c1 < nblk) fetch(c1, Bn);
-        }
-    }
-    // The new token (fused owner split): one more block of one token, read
-    // from LDS unquantised (as full_attention_4b.hip:5351-5353 does), on wave 0.
-    if (owner && wave == 0) {
-        op_t kbn[KSTEPS];
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            u32x4_v w;
-            const int d0 = kdim<FP8>(s, lane >> 4);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(kn_s[d0 + 2 * j], kn_s[d0 + 2 * j + 1]);
-            kbn[s] = as_op<op_t>(w);
-        }
-        process(1, kbn, 1.f, 1.f, [&](int j, float (&vf)[8]) {
-            const bool mine = TPI * j + vt == 0;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vf[e] = mine ? vn_s[vd + e] : 0.f;
-        });
-    }
-
-    // ---------------------------------------------------------------- merge
-    float ltot[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
-#pragma unroll
-    for (int off = LPT; off < 64; off <<= 1)
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
-
-    if ((lane & 15) == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int h = 4 * (lane >> 4) + i;
-            if (h < GP) {
-                ml_s[wave][h][0] = m[i];
-                ml_s[wave][h][1] = ltot[i];
-            }
-        }
-    }
-    __syncthreads();
-    float fw[GP];
-#pragma unroll
-    for (int h = 0; h < GP; ++h) {
-        float M = ml_s[0][h][0];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
-        fw[h] = exp2f(ml_s[wave][h][0] - M);
-    }
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
-
-    // One LDS round: every wave parks its scaled sums in its own slot, then
-    // the whole workgroup adds the NW slots and writes the split's partials.
-    if (lane < LPT) {
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) smem[(wave * GP + h) * D + vd + e] = acc[h][e];
-    }
-    __syncthreads();
-    for (int idx = tid; idx < G * D; idx += NT) {
-        const int h = idx / D, d = idx % D;
-        float o = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) o += smem[(w * GP + h) * D + d];
-        const int64_t row = pre_b * p.Hq + static_cast<int64_t>(kvh * G + h) * n_b + split;
-        store_agent(p.part_o + row * D + d, o);
-    }
-    if (wave == 0) {
-        if (lane < G) {
-            const int h = lane;
-            float M = -1e30f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
-            float L = 0.f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) L += exp2f(ml_s[w][h][0] - M) * ml_s[w][h][1];
-            const int64_t row = pre_b * p.Hq + static_cast<int64_t>(kvh * G + h) * n_b + split;
-            store_agent(&p.part_ml[2 * row], M);
-            store_agent(&p.part_ml[2 * row + 1], L);
-        }
-    }
-
-    // ---------------------------------------------------------------- split merge
-    // The last split of (b, kv head) to arrive merges all of them (log-sum-exp)
-    // and applies the gate.  The partials are written and read with device-
-    // coherent (sc1) accesses, and the writer waits for its stores to complete
-    // before it arrives, so no device-wide fence (an L2 writeback and
-    // invalidate on this GPU) is needed.
-    __shared__ int last_s;
-    const int ns = (len + chunk - 1) / chunk;  // splits that hold tokens (<= n_b)
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&p.arrivals[b * p.Hkv + kvh], 1u);
-        last_s = prev == static_cast<unsigned>(ns - 1);
-    }
-    __syncthreads();
-    if (!last_s) return;
-    // One online pass over the splits of each head, MCH at a time with all
-    // their loads in flight together.  With at least twice as many waves as
-    // heads, two waves share a head (half its dims each) and take 32 splits a
-    // round.  The gate is loaded before the partials, so its round trip is
-    // not the last one.
-    auto merge_head = [&](const int hh, const int part, auto mch_tag, auto dpw_tag) {
-        constexpr int MCH = decltype(mch_tag)::value;
-        constexpr int DPW = decltype(dpw_tag)::value;  // dims per lane handled by this wave
-        const int h = kvh * G + hh;
-        const int64_t row0 = pre_b * p.Hq + static_cast<int64_t>(h) * n_b;
-        float gv[DPW];
-#pragma unroll
-        for (int k = 0; k < DPW; ++k)
-            gv[k] = p.gate ? bf16_bits_to_f32(p.gate[b * p.g_bstride + h * p.g_hstride + lane + 64 * (part * DPW + k)])
-                           : 0.f;
-        float M = -1e30f, Ls = 0.f, o[DPW];
-#pragma unroll
-        for (int k = 0; k < DPW; ++k) o[k] = 0.f;
-        for (int s0 = 0; s0 < ns; s0 += MCH) {
-            float ms[MCH], ls[MCH], os[MCH][DPW];
-#pragma unroll
-            for (int c = 0; c < MCH; ++c) {
-                const int sc = min(s0 + c, ns - 1);  // duplicates past ns get zero weight below
-                ms[c] = load_agent(&p.part_ml[2 * (row0 + sc)]);
-                ls[c] = load_agent(&p.part_ml[2 * (row0 + sc) + 1]);
-#pragma unroll
-                for (int k = 0; k < DPW; ++k)
-                    os[c][k] = load_agent(&p.part_o[(row0 + sc) * D + lane + 64 * (part * DPW + k)]);
-            }
-            float mc = M;
-#pragma unroll
-            for (int c = 0; c < MCH; ++c)
-                if (s0 + c < ns) mc = fmaxf(mc, ms[c]);
-            const float a = __builtin_amdgcn_exp2f(M - mc);
-            Ls *= a;
-#pragma unroll
-            for (int k = 0; k < DPW; ++k) o[k] *= a;
-#pragma unroll
-            for (int c = 0; c < MCH; ++c) {
-                const float f = s0 + c < ns ? __builtin_amdgcn_exp2f(ms[c] - mc) : 0.f;
-                Ls = fmaf(f, ls[c], Ls);
-#pragma unroll
-                for (int k = 0; k < DPW; ++k) o[k] = fmaf(f, os[c][k], o[k]);
-            }
-            M = mc;
-        }
-        const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
-#pragma unroll
-        for (int k = 0; k < DPW; ++k) {
-            const int d = lane + 64 * (part * DPW + k);
-            float r = o[k] * inv;
-            if (p.gate) {
-                // bf16(bf16(attn) * sigmoid(gate)) (full_attention_4b.hip:5464-5470)
-                r = bf16_round(bf16_round(r) * (1.0f / (1.0f + expf(-gv[k]))));
-            }
-            store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + d, r);
-        }
-    };
-    constexpr int DPL = D / 64;  // dims per lane of a whole head
-    if constexpr (DPL % 2 == 0) {
-        if (2 * G <= NW) {
-            if (wave < 2 * G)
-                merge_head(wave >> 1, wave & 1, std::integral_constant<int, 32>{}, std::integral_constant<int, DPL / 2>{});
-        } else {
-            for (int hh = wave; hh < G; hh += NW)
-                merge_head(hh, 0, std::integral_constant<int, 16>{}, std::integral_constant<int, DPL>{});
-        }
-    } else {
-        for (int hh = wave; hh < G; hh += NW)
-            merge_head(hh, 0, std::integral_constant<int, 16>{}, std::integral_constant<int, DPL>{});
-    }
-    if (tid == 0) p.arrivals[b * p.Hkv + kvh] = 0u;  // every split has arrived: ready for the next call
+    __shared__ DecodeLds<D, GP> lds;
+    decode_split_body<QT, FP8, D, GP>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
 // ----------------------------------------------------------------------------

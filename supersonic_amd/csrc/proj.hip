@@ -39,6 +39,7 @@
 
 #include "common.hpp"
 #include "kv_view.hpp"
+#include "skinny.hpp"
 #include "supersonic_attn.h"
 
 namespace ssa {
@@ -59,25 +60,27 @@ struct SkinnyParams {
     int64_t x_bs, w_bs, o_bs;  // batch strides in elements
 };
 
-constexpr int kSkinnyWaves = 8;
+template <typename OT, bool RES, bool ROPE = false>
+__global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_eu(4))) void skinny_lds_kernel(SkinnyLdsParams p, RopeEpi e) {
+    __shared__ SkinnyLds lds;
+    skinny_lds_body<OT, RES, ROPE>(p, e, blockIdx.x, blockIdx.z, lds);
+}
+
 constexpr int kSkinnyCB = 1;                        // 16-column blocks per workgroup
 constexpr int kSkinnyKP = kSkinnyWaves / kSkinnyCB;  // k parts per workgroup (one per wave group)
-constexpr int kSkinnySteps = 8;                     // 32-wide k-steps per load batch (<= 128 VGPRs)
-constexpr int kSkinnyCols = 16 * kSkinnyCB;         // W rows (output columns) per workgroup
 constexpr int kSkinnyMaxM = 64;                     // hard limit (4 row blocks)
 constexpr int kSkinnyDefaultM = 12;                 // measured crossover with hipBLASLt
 constexpr size_t kSkinnyArrivalBytes = 64 << 10;  // counters at a fixed offset, ahead of the partials
 
-__device__ __forceinline__ bf16x8_v as_bf16x8(const u32x4_v& v) { return __builtin_bit_cast(bf16x8_v, v); }
 
 template <typename OT, bool RES>
 __device__ __forceinline__ void skinny_store(const SkinnyParams& p, int seg, int b, int row, int col, float s) {
-    const int n = p.n_seg[seg];
+    const int n = pick3(p.n_seg, seg);
     if (row >= p.m || col >= n) return;
     float y = bf16_round(s);
     const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * n + col;
     if constexpr (RES) y = bf16_round(load_f32<OT>(static_cast<const OT*>(p.res), o) + y);
-    store_f32<OT>(static_cast<OT*>(p.out[seg]), o, y);
+    store_f32<OT>(static_cast<OT*>(pick3(p.out, seg)), o, y);
 }
 
 // Workgroup (column block cb, k slice ks, batch b): 64 W rows x `slice` k-steps.
@@ -95,10 +98,10 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_kernel(SkinnyParams 
     const int cbw = wave % kSkinnyCB, kh = wave / kSkinnyCB;
     const int cb = blockIdx.x, ks = blockIdx.y, b = blockIdx.z;
     const int seg = cb < p.cb_end[0] ? 0 : (cb < p.cb_end[1] ? 1 : 2);
-    const int cbs = cb - (seg ? p.cb_end[seg - 1] : 0);  // column block inside the segment
-    const int n = p.n_seg[seg];
+    const int cbs = cb - (seg == 0 ? 0 : (seg == 1 ? p.cb_end[0] : p.cb_end[1]));  // column block inside the segment
+    const int n = pick3(p.n_seg, seg);
     const uint16_t* x = p.x + b * p.x_bs;
-    const uint16_t* w = p.w[seg] + b * p.w_bs;
+    const uint16_t* w = pick3(p.w, seg) + b * p.w_bs;
     const int T = (p.k + 31) / 32;
     const int sb0 = ks * p.slice;
     const int sb1 = min(sb0 + p.slice, T);
@@ -187,21 +190,6 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_kernel(SkinnyParams 
 // chunk's load issued before the reduction (k <= 8192 in one pass of
 // registers; longer rows re-read their chunks from cache).
 template <typename XT>
-__device__ __forceinline__ void load8f(const XT* p, float (&f)[8]);
-template <>
-__device__ __forceinline__ void load8f<bf16_t>(const bf16_t* p, float (&f)[8]) { unpack8<bf16_t>(ld16(p), f); }
-template <>
-__device__ __forceinline__ void load8f<float>(const float* p, float (&f)[8]) {
-    const f32x4_v a = *reinterpret_cast<const f32x4_v*>(p);
-    const f32x4_v b = *reinterpret_cast<const f32x4_v*>(p + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        f[e] = a[e];
-        f[4 + e] = b[e];
-    }
-}
-
-template <typename XT>
 __global__ __launch_bounds__(256) void input_norm_kernel(int rows, int k, float eps, const XT* x, const uint16_t* w,
                                                          uint16_t* out) {
     __shared__ float part[4];
@@ -264,261 +252,6 @@ __global__ __launch_bounds__(256) void input_norm_kernel(int rows, int k, float 
 // workgroup, measured slower than the separate norm kernel: 30.9 vs 29.2 us
 // for the config-2 Q/K/V step.)
 // ---------------------------------------------------------------------------
-constexpr int kXsMax = 32768;  // staged elements (64 KB): two workgroups per CU
-constexpr int kXsChunks = kXsMax / 8 / 512;  // 16-byte chunks per thread at most
-constexpr int kXsDummy = kXsMax + 120;        // 16-byte slot for the chunks past the rows
-
-// Per-head QK RMSNorm + partial RoPE (+ KV-cache append) applied to the
-// Q/K projection outputs (the fused projection of the decode step).
-struct RopeEpi {
-    uint16_t* q_out;      // [m, Hq*D]   normalised + rotated q
-    uint16_t* gate_out;   // [m, Hq*D]   raw gate half of each q_proj head
-    uint16_t* k_out;      // [m, Hkv*D]  normalised + rotated k
-    uint16_t* v_out;      // [m, Hkv*D]
-    const uint16_t* q_norm_w;
-    const uint16_t* k_norm_w;
-    const uint16_t* cos_t;  // [max_pos, half_rot]
-    const uint16_t* sin_t;
-    const int32_t* pos;     // [m] position of each row (RoPE angle, cache slot)
-    KvView kv;              // bf16 cache the new k / v are appended to (kv.k == NULL: none)
-    unsigned* counters;     // [Hq + Hkv] column-block arrivals per head, zero between calls
-    int Hq, Hkv, D, half_rot;
-    float eps;
-};
-
-__device__ __forceinline__ void store_agent_u32(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// One head row of D bf16 values, lane holding the EPL = D / 64 consecutive
-// dims lane * EPL ..: RMSNorm with (1 + w) (bf16 result), then rotate-half
-// RoPE on dims [0, 2 hr) at position pos (bf16 result), the megakernel's
-// steps B-C (full_attention_4b.hip:5142-5224).  rowbuf: D floats of LDS
-// private to the wave (RoPE partners).
-template <int EPL>
-__device__ __forceinline__ void norm_rope_row(float (&x)[EPL], const uint16_t* w, const uint16_t* cos_t,
-                                              const uint16_t* sin_t, int pos, int hr, float eps, int D,
-                                              float* rowbuf) {
-    const int lane = threadIdx.x & 63;
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) ss += x[j] * x[j];
-    ss = wave_sum(ss);
-    const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
-#pragma unroll
-    for (int j = 0; j < EPL; ++j)
-        x[j] = bf16_round(x[j] * inv * (bf16_bits_to_f32(w[lane * EPL + j]) + 1.0f));
-    if (hr > 0) {
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) rowbuf[lane * EPL + j] = x[j];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            const int d = lane * EPL + j;
-            if (d < 2 * hr) {
-                const int ti = d < hr ? d : d - hr;
-                const float c = bf16_bits_to_f32(cos_t[static_cast<int64_t>(pos) * hr + ti]);
-                const float sn = bf16_bits_to_f32(sin_t[static_cast<int64_t>(pos) * hr + ti]);
-                const float other = rowbuf[d < hr ? d + hr : d - hr];
-                x[j] = d < hr ? bf16_round(x[j] * c - other * sn) : bf16_round(other * sn + x[j] * c);
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-}
-
-struct SkinnyLdsParams {
-    const uint16_t* x;      // [batch][m][k] bf16
-    const uint16_t* w[3];
-    void* out[3];
-    const void* res;
-    int n_seg[3];
-    int cb_end[3];
-    int m, k;
-    int64_t x_bs, w_bs, o_bs;
-};
-
-template <typename OT, bool RES, bool ROPE = false>
-__global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_eu(4))) void skinny_lds_kernel(SkinnyLdsParams p, RopeEpi e) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[kXsMax + 16 * 8];
-    __shared__ __attribute__((aligned(16))) float red[kSkinnyWaves][256];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int cb = blockIdx.x, b = blockIdx.z;
-    const int seg = cb < p.cb_end[0] ? 0 : (cb < p.cb_end[1] ? 1 : 2);
-    const int cbs = cb - (seg ? p.cb_end[seg - 1] : 0);
-    const int n = p.n_seg[seg];
-    const int k = p.k, m = p.m;
-    const int ldx = k + 8;  // padded LDS row: the 16 rows of an A operand read hit distinct banks
-    const int cpr = k / 8;  // 16-byte chunks per row
-    const uint16_t* x = p.x + b * p.x_bs;
-    const u32x4_v zero = {0u, 0u, 0u, 0u};
-
-    // 1. the activation rows (and norm weights), ahead of any W load
-    // Branch-free (clamped addresses, values selected afterwards): conditional
-    // loads and stores would sit in blocks where the wait for these loads
-    // falls back to vmcnt(0), which would also wait for the W batch.
-    const int nch = m * cpr;
-    u32x4_v xr[kXsChunks];
-#pragma unroll
-    for (int j = 0; j < kXsChunks; ++j) {
-        const int c = min(tid + 512 * j, nch - 1);
-        xr[j] = ld16(x + static_cast<int64_t>(c / cpr) * k + 8 * (c % cpr));
-    }
-    asm volatile("" ::: "memory");
-
-    // 2. the first W batch
-    const int T = (k + 31) / 32;
-    const int per = (T + kSkinnyWaves - 1) / kSkinnyWaves;
-    const int s0 = wave * per;
-    const int s1 = min(s0 + per, T);
-    const int col = lane & 15;
-    const int kq = (lane >> 4) * 8;
-    const int n_w = cbs * 16 + col;
-    const uint16_t* wrow = p.w[seg] + b * p.w_bs + static_cast<int64_t>(min(n_w, n - 1)) * k + kq;
-    // Unconditional W loads at a clamped, always in-range address: a step
-    // outside this wave's range (or past k) meets a zero A operand instead.
-    // (A load under a condition would sit in its own block, where waiting for
-    // the activation loads issued before it falls back to vmcnt(0).)
-    const uint16_t* wrow0 = wrow - kq;
-    auto wload = [&](int s) { return ld16(wrow0 + min(s * 32 + kq, k - 8)); };
-    u32x4_v wv[kSkinnySteps];
-#pragma unroll
-    for (int j = 0; j < kSkinnySteps; ++j) wv[j] = wload(s0 + j);
-
-    // 3. stage the rows in LDS; chunks past the rows go to a dummy slot at the
-    // end of the padding.  The padded rows end at m * ldx - 8 = m * k + 8 (m - 1)
-    // <= kXsMax + 120 elements (m <= 16, m * k <= kXsMax), so the slot
-    // [kXsMax + 120, kXsMax + 128) never overlaps a row.
-#pragma unroll
-    for (int j = 0; j < kXsChunks; ++j) {
-        const int c = tid + 512 * j;
-        st16(c < nch ? xs + (c / cpr) * ldx + 8 * (c % cpr) : xs + kXsDummy, xr[j]);
-    }
-    lds_barrier();
-
-    // 4. the weight stream, A operand from LDS
-    const bool mvalid = col < m;
-    const uint16_t* xrow = xs + col * ldx + kq;
-    f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
-    for (int sb = s0; sb < s1; sb += kSkinnySteps) {
-        if (sb > s0) {
-#pragma unroll
-            for (int j = 0; j < kSkinnySteps; ++j) wv[j] = wload(sb + j);
-        }
-#pragma unroll
-        for (int j = 0; j < kSkinnySteps; ++j) {
-            const int s = sb + j;
-            const u32x4_v a = (s < s1 && mvalid && s * 32 + kq < k)
-                                  ? *reinterpret_cast<const u32x4_v*>(xrow + s * 32) : zero;
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(wv[j]), acc, 0, 0, 0);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][(4 * (lane >> 4) + i) * 16 + col] = acc[i];
-    __syncthreads();
-    if constexpr (!ROPE) {
-        if (tid < 256) {
-            const int row = tid >> 4, c = cbs * 16 + (tid & 15);
-            if (row < m && c < n) {
-                float sum = 0.f;
-#pragma unroll
-                for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][tid];
-                float y = bf16_round(sum);
-                const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * n + c;
-                if constexpr (RES) y = bf16_round(load_f32<OT>(static_cast<const OT*>(p.res), o) + y);
-                store_f32<OT>(static_cast<OT*>(p.out[seg]), o, y);
-            }
-        }
-    } else {
-        // Segments: 0 = W_q (per head [q | gate], 2D columns), 1 = W_k, 2 = W_v.
-        // A 16-column block lies inside one head and one half of it.
-        const int D = e.D;
-        const int c0 = cbs * 16;
-        const int hq = seg == 0 ? c0 / (2 * D) : c0 / D;   // head of the block
-        const bool is_q = seg == 0 && (c0 % (2 * D)) < D;
-        const bool is_gate = seg == 0 && !is_q;
-        const bool norm_block = is_q || seg == 1;           // its head is normalised once complete
-        if (tid < 256) {
-            const int row = tid >> 4, cc = tid & 15;
-            float sum = 0.f;
-#pragma unroll
-            for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][tid];
-            const uint32_t yb = f32_to_bf16_bits(sum);          // the projection's bf16 rounding
-            const uint32_t pair = yb | (static_cast<uint32_t>(__shfl_xor(static_cast<int>(yb), 1)) << 16);
-            if (row < m) {
-                const int d = (seg == 0 ? c0 % (2 * D) : c0 % D) + cc - (is_gate ? D : 0);
-                const int64_t hd = static_cast<int64_t>(row) * (seg == 0 ? e.Hq : e.Hkv) * D + hq * D + d;
-                if (norm_block) {
-                    // pre-norm values, device-coherent: the head's last block reads them back
-                    uint16_t* dst = seg == 0 ? e.q_out : e.k_out;
-                    if ((cc & 1) == 0) store_agent_u32(reinterpret_cast<uint32_t*>(dst + hd), pair);
-                } else if (is_gate) {
-                    e.gate_out[hd] = static_cast<uint16_t>(yb);
-                } else {
-                    e.v_out[hd] = static_cast<uint16_t>(yb);
-                    if (e.kv.k) {
-                        const int64_t o = e.kv.row(row, hq, e.pos[row], D) + d;
-                        reinterpret_cast<uint16_t*>(e.kv.v)[o] = static_cast<uint16_t>(yb);
-                    }
-                }
-            }
-        }
-        if (!norm_block) return;
-        // the head's last column block to arrive normalises and rotates it
-        __shared__ int last_s;
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
-        __syncthreads();
-        const int ctr = seg == 0 ? hq : e.Hq + hq;
-        if (tid == 0) {
-            const unsigned prev = atomicAdd(&e.counters[ctr], 1u);
-            last_s = prev == static_cast<unsigned>(D / 16 - 1);
-            if (last_s) e.counters[ctr] = 0u;  // every block of the head has arrived
-        }
-        __syncthreads();
-        if (!last_s) return;
-        float* rowbuf = reinterpret_cast<float*>(xs) + wave * D;  // the activations are no longer read
-        uint16_t* dst = seg == 0 ? e.q_out : e.k_out;
-        const uint16_t* nw = seg == 0 ? e.q_norm_w : e.k_norm_w;
-        const int H = seg == 0 ? e.Hq : e.Hkv;
-        for (int row = wave; row < m; row += kSkinnyWaves) {
-            uint16_t* rp = dst + static_cast<int64_t>(row) * H * D + hq * D;
-            const int pos = e.pos[row];
-            auto run = [&](auto epl_tag) {
-                constexpr int EPL = decltype(epl_tag)::value;
-                float x[EPL];
-                if constexpr (EPL == 4) {
-                    const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(rp) + lane, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) x[j] = bf16_bits_to_f32(static_cast<uint32_t>(v >> (16 * j)) & 0xFFFFu);
-                } else {
-                    const uint32_t v = __hip_atomic_load(reinterpret_cast<uint32_t*>(rp) + lane, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-                    x[0] = bf16_bits_to_f32(v & 0xFFFFu);
-                    x[1] = bf16_bits_to_f32(v >> 16);
-                }
-                norm_rope_row<EPL>(x, nw, e.cos_t, e.sin_t, pos, e.half_rot, e.eps, D, rowbuf);
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) {
-                    rp[lane * EPL + j] = static_cast<uint16_t>(f32_to_bf16_bits(x[j]));
-                    if (seg == 1 && e.kv.k) {
-                        const int64_t o = e.kv.row(row, hq, pos, D) + lane * EPL + j;
-                        reinterpret_cast<uint16_t*>(e.kv.k)[o] = static_cast<uint16_t>(f32_to_bf16_bits(x[j]));
-                    }
-                }
-            };
-            if (D == 256) run(std::integral_constant<int, 4>{});
-            else run(std::integral_constant<int, 2>{});
-        }
-    }
-}
-
 // Unfused path of the same epilogue (rows past the LDS-staged kernel, head
 // dims other than 128/256): one wave per (row, head) over the plain
 // projection outputs.  Blocks 0 .. Hq-1 of a row: q head (q_proj [m, Hq*2D]

@@ -105,6 +105,10 @@ SIGNATURES = {
     "supersonic_attn_gfx950_qkv_proj_rope":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
          _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p, _sz],
+    "supersonic_attn_gfx950_decode_layer_workspace_size": [_sz, _sz, _sz, _sz, _sz, _sz],
+    "supersonic_attn_gfx950_decode_layer":
+        [_sz, _p, _i, _i, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+         _p, C.POINTER(KvCacheDesc), _p, _sz],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "supersonic_attn_gfx950_set_profile_events": [_p, _p],
     "supersonic_attn_rope_tables": [_sz, _sz, C.c_double, _p, _p],
@@ -112,7 +116,8 @@ SIGNATURES = {
 }
 RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_gfx950_prefill_workspace_size": _sz,
             "supersonic_attn_gfx950_o_proj_workspace_size": _sz, "supersonic_attn_gfx950_qkv_proj_workspace_size": _sz,
-            "supersonic_attn_gfx950_qkv_proj_rope_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
+            "supersonic_attn_gfx950_qkv_proj_rope_workspace_size": _sz,
+            "supersonic_attn_gfx950_decode_layer_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
             "supersonic_attn_gfx950_set_profile_events": None}
 
 _LIB = None
@@ -421,6 +426,27 @@ def qkv_proj_rope(ordinal, hidden, input_norm_w, q_proj_w, k_proj_w, v_proj_w, q
 def qkv_proj_rope_workspace_size(rows, hidden_dim, q_heads, kv_heads, head_dim) -> int:
     return int(load().supersonic_attn_gfx950_qkv_proj_rope_workspace_size(rows, hidden_dim, q_heads, kv_heads,
                                                                          head_dim))
+
+
+def decode_layer_workspace_size(batch, hidden_dim, q_heads, kv_heads, head_dim, max_kv_len) -> int:
+    return int(load().supersonic_attn_gfx950_decode_layer_workspace_size(batch, hidden_dim, q_heads, kv_heads,
+                                                                        head_dim, max_kv_len))
+
+
+def decode_layer(ordinal, hidden, input_norm_w, q_proj_w, k_proj_w, v_proj_w, q_norm_w, k_norm_w, o_proj_w,
+                 cos_table, sin_table, positions, cache: "KvCache", workspace, *, q_heads, kv_heads, head_dim,
+                 rotary_dim, max_kv_len, eps=1e-6, qk_eps=1e-6, scale=None, stream=None):
+    """``supersonic_attn_gfx950_decode_layer``: the persistent one-kernel decode layer (hidden updated in place)."""
+    import torch
+    B, hid = hidden.shape
+    scale = head_dim ** -0.5 if scale is None else scale
+    hd = {torch.bfloat16: ScalarType.BF16, torch.float32: ScalarType.F32}[hidden.dtype]
+    desc = cache.desc()
+    _check("decode_layer", load().supersonic_attn_gfx950_decode_layer(
+        ordinal, _stream_ptr(stream), hd, KV_FP8_E4M3 if cache.fp8 else KV_BF16, B, hid, q_heads, kv_heads,
+        head_dim, rotary_dim, max_kv_len, eps, qk_eps, scale, _ptr(hidden), _ptr(input_norm_w), _ptr(q_proj_w),
+        _ptr(k_proj_w), _ptr(v_proj_w), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(o_proj_w), _ptr(cos_table),
+        _ptr(sin_table), _ptr(positions), C.byref(desc), *_ws(workspace)))
 
 
 def quantize_kv_fp8_ocp(ordinal, src, dst_fp8, dst_scale, num_kv_heads, seq_len, head_dim, max_t, pos_offset,

@@ -1,0 +1,134 @@
+"""GPU parity of the persistent decode layer (supersonic_attn_gfx950_decode_layer)
+through the C ABI against the oracle's layer chain: input RMSNorm + Q/K/V
+projections (oracle.qkv_proj), the decode step (oracle.decode_layer: QK norm,
+RoPE, KV append, attention, gate) and o_proj + residual (oracle.o_proj_residual).
+
+Bar: the updated hidden rows within 2e-2 x max(1, max|ref|) max-abs and 2e-3
+mean-abs (BF16 KV; 4e-2 / 4e-3 for FP8 KV, as the decode tests state); the
+appended V rows (the layer's own projection) within two bf16 ulps + 2^-10 of
+the oracle's (the bar of the projection tests), at least 75% identical (the input
+norm is summed in another order than the oracle's, which moves a few more roundings).  Two calls in a row on one workspace check that the
+barrier and split counters are left at zero."""
+import pytest
+import torch
+
+from gpu_util import DEV, announce, dev, fp8_rows, gen
+from oracle import attn_oracle as O
+from supersonic_amd import kernel_ffi as K
+
+pytestmark = pytest.mark.gpu
+
+
+def layer_case(seed, B, Hq, Hkv, D, rot, hid, lens, fp8=False, hidden_f32=False):
+    g = gen(seed)
+    cap = max(lens) + 1
+    c = dict(B=B, Hq=Hq, Hkv=Hkv, D=D, rot=rot, hid=hid, lens=lens, fp8=fp8)
+    c["hidden"] = O.randn_bf16(g, B, hid)
+    c["nw"] = O.randn_bf16(g, hid, std=0.1)
+    c["wq"], c["wk"], c["wv"] = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (Hq * 2 * D, Hkv * D, Hkv * D))
+    c["wo"] = O.randn_bf16(g, hid, Hq * D, std=(Hq * D) ** -0.5)
+    c["qw"], c["kw"] = O.norm_weights(g, D)
+    c["cos"], c["sin"] = O.rope_tables(rot, cap + 1, 1.0e7)
+    kc = O.randn_bf16(g, B, Hkv, cap, D)
+    vc = O.randn_bf16(g, B, Hkv, cap, D)
+    if fp8:
+        c["k"], c["ks"] = fp8_rows(kc)
+        c["v"], c["vs"] = fp8_rows(vc)
+    else:
+        c["k"], c["v"], c["ks"], c["vs"] = kc, vc, None, None
+    c["hidden_dtype"] = torch.float32 if hidden_f32 else torch.bfloat16
+    return c
+
+
+def run_layer(c, ws):
+    cache = K.KvCache(dev(c["k"]), dev(c["v"]), dev(c["ks"]), dev(c["vs"]))
+    h = c["hidden"].to(c["hidden_dtype"]).to(DEV)
+    pos = torch.tensor(c["lens"], dtype=torch.int32, device=DEV)
+    K.decode_layer(0, h, dev(c["nw"]), dev(c["wq"]), dev(c["wk"]), dev(c["wv"]), dev(c["qw"]), dev(c["kw"]),
+                   dev(c["wo"]), dev(c["cos"]), dev(c["sin"]), pos, cache, ws, q_heads=c["Hq"], kv_heads=c["Hkv"],
+                   head_dim=c["D"], rotary_dim=c["rot"], max_kv_len=max(c["lens"]) + 1)
+    torch.cuda.synchronize()
+    return h.float().cpu(), cache
+
+
+def oracle_layer(c):
+    B = c["B"]
+    shape = O.LayerShape(c["Hq"], c["Hkv"], c["D"], c["rot"])
+    rq, rk, rv = O.qkv_proj(c["hidden"], c["nw"], c["wq"], c["wk"], c["wv"])
+    k = c["k"].clone()
+    v = c["v"].clone()
+    ks = None if c["ks"] is None else [c["ks"][b].clone() for b in range(B)]
+    vs = None if c["vs"] is None else [c["vs"][b].clone() for b in range(B)]
+    ra = O.decode_layer(shape, rq, rk, rv, c["qw"], c["kw"], c["cos"], c["sin"], c["lens"],
+                        [k[b] for b in range(B)], [v[b] for b in range(B)], ks, vs, codec="ocp")
+    return O.o_proj_residual(ra, c["wo"], c["hidden"]), v
+
+
+def check_layer(c, out, cache, ref, v_ref):
+    d = (out - ref).abs()
+    scale = max(1.0, ref.abs().max().item())
+    tol = (4e-2, 4e-3) if c["fp8"] else (2e-2, 2e-3)
+    assert d.max().item() <= tol[0] * scale and d.mean().item() <= tol[1], \
+        f"layer: max {d.max().item():.3e} mean {d.mean().item():.3e}"
+    for b, p in enumerate(c["lens"]):
+        # the appended V row is this layer's own projection: within the projection's
+        # rounding (fp32 summation order) of the oracle's (fp8: one code)
+        got, want = cache.v[b, :, p].cpu(), v_ref[b, :, p]
+        if c["fp8"]:
+            assert (got.int() - want.int()).abs().max().item() <= 1 or (got != want).float().mean().item() < 0.02
+        else:
+            gf, wf = got.float(), want.float()
+            ulp = torch.exp2(torch.floor(torch.log2(wf.abs().clamp_min(2.0 ** -100))) - 7)
+            assert bool(((gf - wf).abs() <= 2 * ulp + 2.0 ** -10).all()), (gf - wf).abs().max().item()
+            assert (gf == wf).float().mean().item() > 0.75
+
+
+CASES = {
+    "config1": dict(B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[2048]),
+    "config2_b4_ragged": dict(B=4, Hq=16, Hkv=4, D=256, rot=64, hid=4096, lens=[3000, 17, 1500, 0]),
+    "d128": dict(B=2, Hq=8, Hkv=2, D=128, rot=32, hid=2048, lens=[700, 2100]),
+    "fp8": dict(B=2, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[1200, 333], fp8=True),
+    "f32_hidden": dict(B=3, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[64, 65, 900], hidden_f32=True),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_decode_layer_matches_oracle_chain(name):
+    kw = CASES[name]
+    announce(f"persistent decode layer {name}: {kw}")
+    c = layer_case(130, **kw)
+    ws = torch.zeros(K.decode_layer_workspace_size(c["B"], c["hid"], c["Hq"], c["Hkv"], c["D"], max(c["lens"]) + 1),
+                     dtype=torch.uint8, device=DEV)
+    out, cache = run_layer(c, ws)
+    ref, v_ref = oracle_layer(c)
+    check_layer(c, out, cache, ref, v_ref)
+    assert int(ws[:256].count_nonzero()) == 0, "barrier counters not reset"
+
+
+def test_decode_layer_twice_on_one_workspace():
+    """Two layers back to back on one workspace, the second smaller: the barrier
+    and split counters each call leaves at zero serve the next."""
+    cs = [layer_case(131, B=4, Hq=16, Hkv=4, D=256, rot=64, hid=4096, lens=[1000, 2000, 5, 4095]),
+          layer_case(132, B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[300])]
+    n = max(K.decode_layer_workspace_size(c["B"], c["hid"], c["Hq"], c["Hkv"], c["D"], max(c["lens"]) + 1) for c in cs)
+    ws = torch.zeros(n, dtype=torch.uint8, device=DEV)
+    for i, c in enumerate(cs):
+        announce(f"persistent decode layer, call {i}")
+        out, cache = run_layer(c, ws)
+        ref, v_ref = oracle_layer(c)
+        check_layer(c, out, cache, ref, v_ref)
+
+
+def test_decode_layer_rejects_unsupported_shapes():
+    lib = K.load()
+    z = torch.zeros(64, device=DEV)
+    p = z.data_ptr()
+    desc = K.KvCacheDesc()
+    desc.k = desc.v = p
+    call = lambda B, hid, hq=8, hkv=2, hd=256: lib.supersonic_attn_gfx950_decode_layer(
+        0, None, 2, 2, B, hid, hq, hkv, hd, 64, 100, 1e-6, 1e-6, 0.0625, p, p, p, p, p, p, p, p, p, p, p,
+        K.C.byref(desc), p, 1 << 30)
+    assert call(17, 1024) == K.ERR["RANGE"]           # more rows than the staged weight stream takes
+    assert call(8, 8192) == K.ERR["RANGE"]            # rows * hidden > 32768
+    assert call(1, 1024, hq=16, hkv=2) == K.ERR["HEADS"]
+    assert call(1, 1024, hd=64) == K.ERR["HEAD_DIM"]
