@@ -163,6 +163,51 @@ __device__ __forceinline__ uint16_t load_agent_u16(const uint16_t* p) {
 __device__ __forceinline__ void store_agent_u16(uint16_t* p, uint16_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void store_agent_u32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_agent_u32(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split partials travel as the bitwise complement of the float's bits (a NaN
+// made canonical first), so a word of zero means "not written yet": a reader
+// polls for its data instead of every writer waiting for its stores to
+// complete before it signals.  Readers set the words back to zero.
+__device__ __forceinline__ uint32_t part_enc(float v) { return ~(v != v ? 0x7fc00000u : __float_as_uint(v)); }
+__device__ __forceinline__ float part_dec(uint32_t w) { return __uint_as_float(~w); }
+__device__ __forceinline__ void store_part(float* p, float v) { store_agent_u32(reinterpret_cast<uint32_t*>(p), part_enc(v)); }
+constexpr int kMergePoll = 1 << 16;
+
+// Device-coherent (sc1) vector accesses of 4 << L2B bytes per lane through a
+// buffer resource on a wave-uniform base: one instruction for a lane's
+// 4-16 bytes (coherent accesses cost about as much per instruction as per
+// dword, so wide ones pay).
+template <int N> struct U32N { typedef uint32_t t __attribute__((ext_vector_type(N))); };
+template <> struct U32N<1> { typedef uint32_t t; };
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* uniform_base) {
+    const uint64_t a = reinterpret_cast<uint64_t>(uniform_base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+    void* u = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, static_cast<short>(0), 0x7fffffff, 0x00020000);
+}
+constexpr int kSc1 = 0x10;  // cache-policy bit: device-coherent access
+template <int N>
+__device__ __forceinline__ typename U32N<N>::t ld_coh(const void* uniform_base, int byte_off) {
+    const __amdgpu_buffer_rsrc_t r = coh_rsrc(uniform_base);
+    if constexpr (N == 4) return __builtin_bit_cast(typename U32N<N>::t, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1));
+    else if constexpr (N == 2) return __builtin_bit_cast(typename U32N<N>::t, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kSc1));
+    else return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kSc1);
+}
+template <int N>
+__device__ __forceinline__ void st_coh(void* uniform_base, int byte_off, typename U32N<N>::t v) {
+    const __amdgpu_buffer_rsrc_t r = coh_rsrc(uniform_base);
+    if constexpr (N == 4) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, v), r, byte_off, 0, kSc1);
+    else if constexpr (N == 2) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_v, v), r, byte_off, 0, kSc1);
+    else __builtin_amdgcn_raw_buffer_store_b32(v, r, byte_off, 0, kSc1);
+}  // bounded poll of a merge for partials in flight
+
 __device__ __forceinline__ u32x4_v ld16_agent(const void* p) {
     uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<void*>(p));
     const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

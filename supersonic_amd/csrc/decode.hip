@@ -389,8 +389,8 @@ std::vector<void*> g_scratch_ptr;  // device address of `scratch`, per device
 
 // Device address of this device's `scratch` (the current device must be
 // `device`), looked up once per device.  The first lookup on a device also
-// clears the arrival counters with a kernel on `st` (every later call leaves
-// them at zero).  NULL if the lookup fails.
+// clears the array (arrival counters and partial slots) with a kernel on `st`
+// (every later call leaves them at zero).  NULL if the lookup fails.
 static void* scratch_for(int device, hipStream_t st) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (device < 0) return nullptr;
@@ -398,7 +398,8 @@ static void* scratch_for(int device, hipStream_t st) {
     if (!g_scratch_ptr[device]) {
         void* ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
-        hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, st, static_cast<unsigned*>(ptr), kMaxArrivals);
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(256), dim3(256), 0, st, static_cast<unsigned*>(ptr),
+                           static_cast<int>(kScratchBytes / sizeof(unsigned)));
         if (hipGetLastError() != hipSuccess) return nullptr;
         g_scratch_ptr[device] = ptr;
     }

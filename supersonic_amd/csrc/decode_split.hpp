@@ -129,7 +129,7 @@ struct DecodeLds {
     float ml_s[NW][GP][2];
     u32x4_v qop_s[(D / 32) * 64];   // Q as the MFMA A operand
     int next_blk;                   // next 16-token block to claim
-    int plan_s[7];
+    int plan_s[8];
     int last_s;
 };
 
@@ -142,6 +142,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                                                   DecodeLds<D, GP>& L) {
     static_assert(D % 64 == 0 && D <= 512, "head_dim");
     static_assert(GP == 4 || GP == 8 || GP == 16, "padded group");
+    static_assert(decode_waves(GP) * GP >= 16, "smem holds the 16 padded Q rows");
     typedef typename Mfma<QT>::op op_t;
     constexpr int KSTEPS = D / 32;
     constexpr int LPT = D / 8;       // lanes per token row in the V layout
@@ -161,7 +162,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Work item (b, kv head, split), chunk length, and the partial rows of
     // sequence b: pre_b splits before it, n_b of its own per head.
-    int split, kvh, b, chunk, n_b;
+    int split, kvh, b, chunk, n_b, len;
     int64_t pre_b;
     if (p.ragged) {
         // Every workgroup plans the same way from the lengths: chunk =
@@ -170,13 +171,16 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         // head, each of them ceil(len_b / n_b) tokens (rounded up to 16), items
         // are ordered (b, kv head, split), and workgroup i takes item i (past
         // the last item it has nothing to do).
-        int (&plan_s)[7] = L.plan_s;
+        int (&plan_s)[8] = L.plan_s;
         if (wave == 0) {
+            // Up to 64 sequences (the usual case) the lengths are loaded once
+            // and kept in a register: every pass below would otherwise be
+            // another dependent load.
+            const bool one = p.B <= 64;
+            const int l0 = lane < p.B ? max(p.lens[lane] + p.len_plus, 0) : 0;
+            auto len_of = [&](int bi) { return one ? l0 : (bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0); };
             int64_t tot = 0;
-            for (int b0 = 0; b0 < p.B; b0 += 64) {
-                const int bi = b0 + lane;
-                tot += bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
-            }
+            for (int b0 = 0; b0 < p.B; b0 += 64) tot += len_of(b0 + lane);
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) tot += __shfl_xor(tot, o);
             // Per-sequence rounding can push the item count past the target
@@ -188,7 +192,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 int64_t items = 0;
                 for (int b0 = 0; b0 < p.B; b0 += 64) {
                     const int bi = b0 + lane;
-                    const int64_t l = bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
+                    const int64_t l = len_of(bi);
                     items += bi < p.B ? max(static_cast<int64_t>(1), (l + c - 1) / c) : 0;
                 }
 #pragma unroll
@@ -204,7 +208,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             int run = 0, run_n = 0;  // items and splits of the sequences before b0
             for (int b0 = 0; b0 < p.B; b0 += 64) {
                 const int bi = b0 + lane;
-                const int l = bi < p.B ? max(p.lens[bi] + p.len_plus, 0) : 0;
+                const int l = len_of(bi);
                 const int n = bi < p.B ? max(1, (l + ch - 1) / ch) : 0;
                 int incl = n;        // inclusive scan of the split counts
 #pragma unroll
@@ -222,6 +226,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                     // the sequence's n splits share its length equally (16-token
                     // blocks), so no split is left with a short remainder
                     plan_s[5] = l > 0 ? ((l + n - 1) / n + 15) / 16 * 16 : ch;
+                    plan_s[6] = l;
                 }
                 const int tot_n = __shfl(incl, 63);
                 run += tot_n * p.Hkv;
@@ -236,6 +241,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         n_b = plan_s[3];
         pre_b = plan_s[4];
         chunk = plan_s[5];
+        len = plan_s[6];
     } else {
         split = vbx;
         kvh = vby;
@@ -243,8 +249,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         chunk = p.chunk;
         n_b = p.nsplit;
         pre_b = static_cast<int64_t>(b) * p.nsplit;
+        len = p.lens[b] + p.len_plus;
     }
-    const int len = p.lens[b] + p.len_plus;
     const int t_begin = split * chunk;
     if (t_begin >= len) {  // uniform: ragged batch, nothing to do
         if (len <= 0 && split == 0) {
@@ -258,6 +264,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         return;
     }
     const int t_end = min(len, t_begin + chunk);
+    const int ns = (len + chunk - 1) / chunk;  // splits that hold tokens (<= n_b)
     const int G = p.G;
     const int pos = len - 1;
     const bool owner = p.fused && pos >= t_begin && pos < t_end;
@@ -418,22 +425,26 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 if (is_k) vn_s[lane + 64 * k] = vx[k];
             }
         };
-        // This wave's first row goes out first, then the wave's first K/V
-        // block: waiting for the row (vmcnt drains in issue order) does not
-        // wait for the block, whose round trip overlaps the norm and RoPE.
+        // Rows past the first NW (large head groups) first, then this wave's
+        // first row, then the wave's first K/V block: waiting for the row
+        // (vmcnt drains in issue order) does not wait for the block, whose
+        // round trip overlaps the norm and RoPE.  No load may follow the
+        // block's before its use: a later load whose register is reused
+        // would make the compiler wait for the block too.
+        for (int r = wave + NW; r < rows; r += NW) {
+            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
+            row_loads(r, x, vx, w, cs, sn);
+            row_compute(r, x, vx, w, cs, sn);
+        }
         {
             float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
             row_loads(min(wave, rows - 1), x, vx, w, cs, sn);
             fetch(max(0, min(wave, nblk - 1)), A);
             if (wave < rows) row_compute(wave, x, vx, w, cs, sn);
         }
-        for (int r = wave + NW; r < rows; r += NW) {
-            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
-            row_loads(r, x, vx, w, cs, sn);
-            row_compute(r, x, vx, w, cs, sn);
-        }
-        // heads G .. GP-1 are zero rows of the padded MFMA operand
-        for (int idx = G * D + tid; idx < GP * D; idx += NT) smem[idx] = 0.f;
+        // heads G .. 15 are zero rows of the padded MFMA operand (smem holds
+        // at least 16 rows)
+        for (int idx = G * D + tid; idx < 16 * D; idx += NT) smem[idx] = 0.f;
     }
     lds_barrier();
     if (p.fused && owner) {
@@ -480,14 +491,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             u32x4_v w;
             const int dk = kdim<FP8>(s, lane >> 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // clamped read and a select: a branch here would make the
-                // compiler wait for the wave's outstanding K/V loads
-                const int hc = min(hh, G - 1);
-                const float a = smem[hc * D + dk + 2 * j];
-                const float c = smem[hc * D + dk + 2 * j + 1];
-                w[j] = hh < G ? pack2<QT>(a, c) : 0u;
-            }
+            for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(smem[hh * D + dk + 2 * j], smem[hh * D + dk + 2 * j + 1]);
             qop_s[s * 64 + lane] = w;
         }
     }
@@ -637,6 +641,13 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     }
 
     // ---------------------------------------------------------------- merge
+    // Arrival: every split of (b, kv head) that holds tokens counts itself in
+    // as its main loop ends (the last wave; its round trip overlaps the
+    // workgroup's reduction below); the last one to arrive keeps its partial
+    // in LDS and merges them all, polling for the others' partials, which are
+    // stored or on their way.
+    unsigned arrival = 0;
+    if (wave == NW - 1 && lane == 0) arrival = atomicAdd(&p.arrivals[b * p.Hkv + kvh], 1u);
     float ltot[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
@@ -671,8 +682,10 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
 
-    // One LDS round: every wave parks its scaled sums in its own slot, then
-    // the whole workgroup adds the NW slots and writes the split's partials.
+    // One LDS round: every wave parks its scaled sums in its own slot; the
+    // split's partial is then the sum of the NW slots.
+    int& last_s = L.last_s;
+    if (wave == NW - 1 && lane == 0) last_s = arrival == static_cast<unsigned>(ns - 1);
     if (lane < LPT) {
 #pragma unroll
         for (int h = 0; h < GP; ++h)
@@ -680,118 +693,200 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             for (int e = 0; e < 8; ++e) smem[(wave * GP + h) * D + vd + e] = acc[h][e];
     }
     __syncthreads();
-    for (int idx = tid; idx < G * D; idx += NT) {
-        const int h = idx / D, d = idx % D;
-        float o = 0.f;
+    // (M, L) of head hh of this split, from the waves' (m, l)
+    auto own_ml = [&](int hh, float& M, float& Lsum) {
+        M = -1e30f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) o += smem[(w * GP + h) * D + d];
-        const int64_t row = pre_b * p.Hq + static_cast<int64_t>(kvh * G + h) * n_b + split;
-        store_agent(p.part_o + row * D + d, o);
-    }
-    if (wave == 0) {
-        if (lane < G) {
-            const int h = lane;
-            float M = -1e30f;
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_s[w][hh][0]);
+        Lsum = 0.f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
-            float L = 0.f;
+        for (int w = 0; w < NW; ++w) Lsum += exp2f(ml_s[w][hh][0] - M) * ml_s[w][hh][1];
+    };
+    // Partials: part_o rows of D floats, part_ml rows of (M, L), both as
+    // part_enc words (zero = not written yet), written and read with
+    // device-coherent (sc1) vector accesses, so no device-wide fence (an L2
+    // writeback and invalidate on this GPU) is needed and no writer waits for
+    // its stores to complete.  A lane holds DV consecutive dims of a row.
+    constexpr int DV = D / 64;
+    typedef typename U32N<DV>::t dv_t;
+    auto row_of = [&](int hh, int sp) { return pre_b * p.Hq + static_cast<int64_t>(kvh * G + hh) * n_b + sp; };
+    if (!last_s) {
+        for (int hh = wave; hh < G; hh += NW) {
+            dv_t w;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) L += exp2f(ml_s[w][h][0] - M) * ml_s[w][h][1];
-            const int64_t row = pre_b * p.Hq + static_cast<int64_t>(kvh * G + h) * n_b + split;
-            store_agent(&p.part_ml[2 * row], M);
-            store_agent(&p.part_ml[2 * row + 1], L);
+            for (int j = 0; j < DV; ++j) {
+                float o = 0.f;
+#pragma unroll
+                for (int ww = 0; ww < NW; ++ww) o += smem[(ww * GP + hh) * D + lane * DV + j];
+                if constexpr (DV == 1) w = part_enc(o);
+                else w[j] = part_enc(o);
+            }
+            st_coh<DV>(p.part_o + row_of(hh, split) * D, lane * DV * 4, w);
         }
+        if (wave == 0 && lane < G) {
+            float M, Lsum;
+            own_ml(lane, M, Lsum);
+            const uint64_t v = part_enc(M) | (static_cast<uint64_t>(part_enc(Lsum)) << 32);
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(&p.part_ml[2 * row_of(lane, split)]), v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
     }
 
     // ---------------------------------------------------------------- split merge
-    // The last split of (b, kv head) to arrive merges all of them (log-sum-exp)
-    // and applies the gate.  The partials are written and read with device-
-    // coherent (sc1) accesses, and the writer waits for its stores to complete
-    // before it arrives, so no device-wide fence (an L2 writeback and
-    // invalidate on this GPU) is needed.
-    int& last_s = L.last_s;
-    const int ns = (len + chunk - 1) / chunk;  // splits that hold tokens (<= n_b)
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&p.arrivals[b * p.Hkv + kvh], 1u);
-        last_s = prev == static_cast<unsigned>(ns - 1);
-    }
-    __syncthreads();
-    if (!last_s) return;
-    // One online pass over the splits of each head, MCH at a time with all
-    // their loads in flight together.  With at least twice as many waves as
-    // heads, two waves share a head (half its dims each) and take 32 splits a
-    // round.  The gate is loaded before the partials, so its round trip is
-    // not the last one.
-    auto merge_head = [&](const int hh, const int part, auto mch_tag, auto dpw_tag) {
-        constexpr int MCH = decltype(mch_tag)::value;
-        constexpr int DPW = decltype(dpw_tag)::value;  // dims per lane handled by this wave
+    // The last split of (b, kv head) merges all of them (log-sum-exp), its own
+    // partial straight from LDS, and applies the gate.  With at least twice as
+    // many waves as heads, two waves share a head, each taking half of the
+    // splits, and combine through LDS.  A wave takes MCH splits a round: one
+    // load for their (M, L) (lane c holds split c's) and one per split for the
+    // dims, polled until no word reads zero; each word read is then set back
+    // to zero for the next call.  The gate goes out with the first round.
+    constexpr int MCH = 16;
+    const int WPH = 2 * G <= NW ? 2 : 1;                 // waves per head
+    const int part = WPH == 2 ? wave % 2 : 0;
+    const int half = WPH == 2 ? (ns + 1) / 2 : ns;
+    const int sp_lo = part * half, sp_hi = min(ns, sp_lo + half);
+    const bool has_gate = p.gate != nullptr;
+    float Mr = -1e30f, Lr = 0.f, orr[DV];               // this wave's running merge
+    int my_h = -1;
+    for (int hh = wave / WPH; hh < G; hh += NW / WPH) {
+        my_h = hh;
         const int h = kvh * G + hh;
-        const int64_t row0 = pre_b * p.Hq + static_cast<int64_t>(h) * n_b;
-        float gv[DPW];
+        // branch-free: without a gate the load reads the output row (a valid
+        // address) and the values are ignored
+        const uint16_t* grow = has_gate ? p.gate + b * p.g_bstride + h * p.g_hstride
+                                        : static_cast<const uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D;
+        uint16_t graw[DV];
 #pragma unroll
-        for (int k = 0; k < DPW; ++k)
-            gv[k] = p.gate ? bf16_bits_to_f32(COH ? load_agent_u16(p.gate + b * p.g_bstride + h * p.g_hstride + lane +
-                                                                      64 * (part * DPW + k))
-                                                  : p.gate[b * p.g_bstride + h * p.g_hstride + lane + 64 * (part * DPW + k)])
-                           : 0.f;
-        float M = -1e30f, Ls = 0.f, o[DPW];
+        for (int j = 0; j < DV; ++j) graw[j] = COH ? load_agent_u16(grow + lane * DV + j) : grow[lane * DV + j];
+        float M = -1e30f, Ls = 0.f;
 #pragma unroll
-        for (int k = 0; k < DPW; ++k) o[k] = 0.f;
-        for (int s0 = 0; s0 < ns; s0 += MCH) {
-            float ms[MCH], ls[MCH], os[MCH][DPW];
+        for (int j = 0; j < DV; ++j) orr[j] = 0.f;
+        if (part == 0) {  // this split's own partial, from LDS
+            own_ml(hh, M, Ls);
 #pragma unroll
-            for (int c = 0; c < MCH; ++c) {
-                const int sc = min(s0 + c, ns - 1);  // duplicates past ns get zero weight below
-                ms[c] = load_agent(&p.part_ml[2 * (row0 + sc)]);
-                ls[c] = load_agent(&p.part_ml[2 * (row0 + sc) + 1]);
+            for (int j = 0; j < DV; ++j) {
+                float o = 0.f;
 #pragma unroll
-                for (int k = 0; k < DPW; ++k)
-                    os[c][k] = load_agent(&p.part_o[(row0 + sc) * D + lane + 64 * (part * DPW + k)]);
+                for (int ww = 0; ww < NW; ++ww) o += smem[(ww * GP + hh) * D + lane * DV + j];
+                orr[j] = o;
             }
+        }
+        const int64_t row0 = row_of(hh, 0);
+        uint32_t* const pml = reinterpret_cast<uint32_t*>(p.part_ml) + 2 * row0;
+        uint32_t* const po = reinterpret_cast<uint32_t*>(p.part_o) + row0 * D;
+        for (int s0 = sp_lo; s0 < sp_hi; s0 += MCH) {
+            u32x2_v mlw;
+            dv_t os[MCH];
+            const int cl = min(lane, MCH - 1);
+            const bool want_l = s0 + cl < sp_hi && s0 + cl != split && lane < MCH;
+            for (int it = 0;; ++it) {
+                mlw = ld_coh<2>(pml, 8 * min(s0 + cl, sp_hi - 1));
+#pragma unroll
+                for (int c = 0; c < MCH; ++c) os[c] = ld_coh<DV>(po + static_cast<int64_t>(min(s0 + c, sp_hi - 1)) * D, lane * DV * 4);
+                bool miss = want_l & ((mlw[0] == 0u) | (mlw[1] == 0u));
+#pragma unroll
+                for (int c = 0; c < MCH; ++c) {
+                    const bool want = s0 + c < sp_hi && s0 + c != split;
+                    bool z = false;
+                    if constexpr (DV == 1) z = os[c] == 0u;
+                    else {
+#pragma unroll
+                        for (int j = 0; j < DV; ++j) z |= os[c][j] == 0u;
+                    }
+                    miss |= want & z;
+                }
+                // every split has arrived, so its partial is stored or on its
+                // way (the cap only guards against a workspace that was not
+                // zero-filled)
+                if (!__builtin_amdgcn_ballot_w64(miss) || it >= kMergePoll) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+            const float m_l = want_l ? part_dec(mlw[0]) : -1e30f;
+            const float l_l = want_l ? part_dec(mlw[1]) : 0.f;
             float mc = M;
 #pragma unroll
-            for (int c = 0; c < MCH; ++c)
-                if (s0 + c < ns) mc = fmaxf(mc, ms[c]);
+            for (int c = 0; c < MCH; ++c) mc = fmaxf(mc, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_l), c)));
             const float a = __builtin_amdgcn_exp2f(M - mc);
             Ls *= a;
 #pragma unroll
-            for (int k = 0; k < DPW; ++k) o[k] *= a;
+            for (int j = 0; j < DV; ++j) orr[j] *= a;
+            const float f_l = want_l ? __builtin_amdgcn_exp2f(m_l - mc) : 0.f;
+            Ls += wave_sum(f_l * l_l);
 #pragma unroll
             for (int c = 0; c < MCH; ++c) {
-                const float f = s0 + c < ns ? __builtin_amdgcn_exp2f(ms[c] - mc) : 0.f;
-                Ls = fmaf(f, ls[c], Ls);
+                const bool want = s0 + c < sp_hi && s0 + c != split;
+                const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f_l), c));
+                if constexpr (DV == 1) orr[0] = fmaf(f, want ? part_dec(os[c]) : 0.f, orr[0]);
+                else {
 #pragma unroll
-                for (int k = 0; k < DPW; ++k) o[k] = fmaf(f, os[c][k], o[k]);
+                    for (int j = 0; j < DV; ++j) orr[j] = fmaf(f, want ? part_dec(os[c][j]) : 0.f, orr[j]);
+                }
             }
             M = mc;
         }
-        const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+        Mr = M;
+        Lr = Ls;
+        auto finish = [&]() {
+            const float inv = Lr > 0.f ? 1.0f / Lr : 0.f;
+            float r[DV];
 #pragma unroll
-        for (int k = 0; k < DPW; ++k) {
-            const int d = lane + 64 * (part * DPW + k);
-            float r = o[k] * inv;
-            if (p.gate) {
-                // bf16(bf16(attn) * sigmoid(gate)) (full_attention_4b.hip:5464-5470)
-                r = bf16_round(bf16_round(r) * (1.0f / (1.0f + expf(-gv[k]))));
+            for (int j = 0; j < DV; ++j) {
+                r[j] = orr[j] * inv;
+                if (has_gate) {
+                    // bf16(bf16(attn) * sigmoid(gate)) (full_attention_4b.hip:5464-5470)
+                    r[j] = bf16_round(bf16_round(r[j]) * (1.0f / (1.0f + expf(-bf16_bits_to_f32(graw[j])))));
+                }
             }
-            if constexpr (COH) store_f32_agent(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + d, r);
-            else store_f32(static_cast<QT*>(p.out), (static_cast<int64_t>(b) * p.Hq + h) * D + d, r);
-        }
-    };
-    constexpr int DPL = D / 64;  // dims per lane of a whole head
-    if constexpr (DPL % 2 == 0) {
-        if (2 * G <= NW) {
-            if (wave < 2 * G)
-                merge_head(wave >> 1, wave & 1, std::integral_constant<int, 32>{}, std::integral_constant<int, DPL / 2>{});
+            const int64_t ob = (static_cast<int64_t>(b) * p.Hq + h) * D + lane * DV;
+#pragma unroll
+            for (int j = 0; j < DV; ++j) {
+                if constexpr (COH) store_f32_agent(static_cast<QT*>(p.out), ob + j, r[j]);
+                else store_f32(static_cast<QT*>(p.out), ob + j, r[j]);
+            }
+        };
+        // the words read go back to zero (this split's own row was never
+        // stored); after the rounds, so that no load of a later round waits
+        // behind these stores
+        auto reset = [&]() {
+            for (int s1 = sp_lo; s1 < sp_hi; s1 += 64)
+                if (s1 + lane < sp_hi && s1 + lane != split) st_coh<2>(pml, 8 * (s1 + lane), u32x2_v{0u, 0u});
+            for (int s1 = sp_lo; s1 < sp_hi; ++s1)
+                if (s1 != split) st_coh<DV>(po + static_cast<int64_t>(s1) * D, lane * DV * 4, dv_t{});
+        };
+        if (WPH == 1) {
+            finish();
+            reset();
         } else {
-            for (int hh = wave; hh < G; hh += NW)
-                merge_head(hh, 0, std::integral_constant<int, 16>{}, std::integral_constant<int, DPL>{});
+            // two waves per head: the second parks (M, L, o) in LDS (smem is
+            // free once every wave has read its own partial), the first
+            // combines and writes the head
+            lds_barrier();
+            float* park = &smem[hh * (D + 2)];
+            if (part == 1) {
+#pragma unroll
+                for (int j = 0; j < DV; ++j) park[lane * DV + j] = orr[j];
+                if (lane == 0) {
+                    park[D] = Mr;
+                    park[D + 1] = Lr;
+                }
+            }
+            lds_barrier();
+            if (part == 0) {
+                const float M2 = park[D], L2 = park[D + 1];
+                const float mm = fmaxf(Mr, M2);
+                const float a1 = __builtin_amdgcn_exp2f(Mr - mm), a2 = __builtin_amdgcn_exp2f(M2 - mm);
+                Lr = Lr * a1 + L2 * a2;
+#pragma unroll
+                for (int j = 0; j < DV; ++j) orr[j] = orr[j] * a1 + park[lane * DV + j] * a2;
+                finish();
+            }
+            reset();
         }
-    } else {
-        for (int hh = wave; hh < G; hh += NW)
-            merge_head(hh, 0, std::integral_constant<int, 16>{}, std::integral_constant<int, DPL>{});
+    }
+    if (WPH == 2 && my_h < 0) {  // waves without a head still take part in the two barriers
+        lds_barrier();
+        lds_barrier();
     }
     if (tid == 0) p.arrivals[b * p.Hkv + kvh] = 0u;  // every split has arrived: ready for the next call
 }

@@ -53,10 +53,6 @@ struct RopeEpi {
     float eps;
 };
 
-__device__ __forceinline__ void store_agent_u32(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // One head row of D bf16 values, lane holding the EPL = D / 64 consecutive
 // dims lane * EPL ..: RMSNorm with (1 + w) (bf16 result), then rotate-half
 // RoPE on dims [0, 2 hr) at position pos (bf16 result), the megakernel's
