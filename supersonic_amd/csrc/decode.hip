@@ -73,6 +73,7 @@ static int decode_target(int waves) {
     // 2048 resident waves: one 8-wave or two 4-wave workgroups per CU
     return std::max(1, env_int("SUPERSONIC_DECODE_TARGET_WGS", 2048 / waves));
 }
+static int decode_deterministic() { return env_int("SUPERSONIC_DECODE_DETERMINISTIC", 0) != 0; }
 static int decode_min_chunk() { return std::max(64, env_int("SUPERSONIC_DECODE_MIN_CHUNK", 128)); }
 
 // Uniform plan (one length for the whole batch): the same split count for
@@ -184,6 +185,7 @@ static int run_decode(DecodeRequest& r) {
     p.B = r.B;
     p.target = decode_target(waves);
     p.min_chunk = decode_min_chunk();
+    p.det = decode_deterministic();
     p.scale_log2 = r.scale * kLog2e;
     p.arrivals = static_cast<unsigned*>(ws);
     p.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes);

@@ -24,6 +24,7 @@ struct DecodeParams {
     // workgroup gets about the same number of tokens whatever the lengths;
     // chunk and nsplit are then unused.
     int ragged, B, target, min_chunk;
+    int det;                  // 1: static block order (bit-reproducible), 0: blocks claimed from an LDS counter
     float scale_log2;         // softmax scale * log2(e)
     int fused;
     const uint16_t* k_new;    // [B, Hkv*D] bf16
@@ -137,9 +138,17 @@ struct DecodeLds {
 // in the uniform plan, or item vbx of the ragged plan.  COH: q / k_new / v_new
 // / gate are read and the output written with device-coherent accesses (they
 // are exchanged with other workgroups of the same kernel).
-template <typename QT, bool FP8, int D, int GP, bool COH = false>
+struct NoMid {
+    __device__ void operator()() const {}
+};
+
+// mid: called by every thread once, after the work item is planned and its
+// first K/V block fetched, before q / k_new / v_new / gate are read (not
+// called when the workgroup has no work item).
+template <typename QT, bool FP8, int D, int GP, bool COH = false, typename Mid = NoMid>
 __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx, int vby, int vbz,
-                                                  DecodeLds<D, GP>& L) {
+                                                  DecodeLds<D, GP>& L, const Mid& mid = Mid()) {
+    constexpr bool kMid = !std::is_same<Mid, NoMid>::value;
     static_assert(D % 64 == 0 && D <= 512, "head_dim");
     static_assert(GP == 4 || GP == 8 || GP == 16, "padded group");
     static_assert(decode_waves(GP) * GP >= 16, "smem holds the 16 padded Q rows");
@@ -431,15 +440,26 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         // round trip overlaps the norm and RoPE.  No load may follow the
         // block's before its use: a later load whose register is reused
         // would make the compiler wait for the block too.
+        // With a mid hook (the persistent layer), the first K/V block is
+        // fetched and the hook (a grid barrier: q, k_new and v_new are
+        // written by another phase) runs before any of the rows is read.
+        if constexpr (kMid) {
+            fetch(max(0, min(wave, nblk - 1)), A);
+            mid();
+        }
         for (int r = wave + NW; r < rows; r += NW) {
             float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
             row_loads(r, x, vx, w, cs, sn);
             row_compute(r, x, vx, w, cs, sn);
         }
-        {
+        if constexpr (!kMid) {
             float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
             row_loads(min(wave, rows - 1), x, vx, w, cs, sn);
             fetch(max(0, min(wave, nblk - 1)), A);
+            if (wave < rows) row_compute(wave, x, vx, w, cs, sn);
+        } else {
+            float x[EPL], vx[EPL], w[EPL], cs[EPL], sn[EPL];
+            row_loads(min(wave, rows - 1), x, vx, w, cs, sn);
             if (wave < rows) row_compute(wave, x, vx, w, cs, sn);
         }
         // heads G .. 15 are zero rows of the padded MFMA operand (smem holds
@@ -598,11 +618,21 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // current block is computed (two register sets, unrolled by two).
     // Blocks are claimed from an LDS counter (wave w starts with block w), so
     // a wave whose loads are served more slowly simply takes fewer blocks and
-    // the waves of the workgroup finish together.
+    // the waves of the workgroup finish together (about 3% faster at config 2
+    // and 4 than a static order).  The claim order changes the fp32 summation
+    // order from run to run; p.det selects the static order (wave w takes
+    // blocks w, w + NW, ...), whose results are identical run to run.
+    int nxt = wave + NW;
     auto take = [&]() {
         int v = 0;
-        if (lane == 0) v = atomicAdd(&next_blk, 1);
-        return __builtin_amdgcn_readfirstlane(v);
+        if (p.det) {
+            v = nxt;
+            nxt += NW;
+        } else {
+            if (lane == 0) v = atomicAdd(&next_blk, 1);
+            v = __builtin_amdgcn_readfirstlane(v);
+        }
+        return v;
     };
     {
         int c0 = wave, c1 = nblk;
@@ -762,15 +792,16 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         float M = -1e30f, Ls = 0.f;
 #pragma unroll
         for (int j = 0; j < DV; ++j) orr[j] = 0.f;
-        if (part == 0) {  // this split's own partial, from LDS
-            own_ml(hh, M, Ls);
+        // this split's own partial, from LDS, merged at its place in split
+        // order (the result does not depend on which split arrives last)
+        float own_m, own_l, own_o[DV];
+        own_ml(hh, own_m, own_l);
 #pragma unroll
-            for (int j = 0; j < DV; ++j) {
-                float o = 0.f;
+        for (int j = 0; j < DV; ++j) {
+            float o = 0.f;
 #pragma unroll
-                for (int ww = 0; ww < NW; ++ww) o += smem[(ww * GP + hh) * D + lane * DV + j];
-                orr[j] = o;
-            }
+            for (int ww = 0; ww < NW; ++ww) o += smem[(ww * GP + hh) * D + lane * DV + j];
+            own_o[j] = o;
         }
         const int64_t row0 = row_of(hh, 0);
         uint32_t* const pml = reinterpret_cast<uint32_t*>(p.part_ml) + 2 * row0;
@@ -802,8 +833,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 if (!__builtin_amdgcn_ballot_w64(miss) || it >= kMergePoll) break;
                 __builtin_amdgcn_s_sleep(2);
             }
-            const float m_l = want_l ? part_dec(mlw[0]) : -1e30f;
-            const float l_l = want_l ? part_dec(mlw[1]) : 0.f;
+            const bool own_lane = lane < MCH && s0 + lane == split && split < sp_hi;  // inside this wave's range
+            const float m_l = want_l ? part_dec(mlw[0]) : (own_lane ? own_m : -1e30f);
+            const float l_l = want_l ? part_dec(mlw[1]) : (own_lane ? own_l : 0.f);
             float mc = M;
 #pragma unroll
             for (int c = 0; c < MCH; ++c) mc = fmaxf(mc, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_l), c)));
@@ -811,16 +843,18 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             Ls *= a;
 #pragma unroll
             for (int j = 0; j < DV; ++j) orr[j] *= a;
-            const float f_l = want_l ? __builtin_amdgcn_exp2f(m_l - mc) : 0.f;
+            const float f_l = want_l || own_lane ? __builtin_amdgcn_exp2f(m_l - mc) : 0.f;
             Ls += wave_sum(f_l * l_l);
 #pragma unroll
             for (int c = 0; c < MCH; ++c) {
                 const bool want = s0 + c < sp_hi && s0 + c != split;
+                const bool own = s0 + c == split && split < sp_hi;
                 const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f_l), c));
-                if constexpr (DV == 1) orr[0] = fmaf(f, want ? part_dec(os[c]) : 0.f, orr[0]);
+                if constexpr (DV == 1) orr[0] = fmaf(f, want ? part_dec(os[c]) : (own ? own_o[0] : 0.f), orr[0]);
                 else {
 #pragma unroll
-                    for (int j = 0; j < DV; ++j) orr[j] = fmaf(f, want ? part_dec(os[c][j]) : 0.f, orr[j]);
+                    for (int j = 0; j < DV; ++j)
+                        orr[j] = fmaf(f, want ? part_dec(os[c][j]) : (own ? own_o[j] : 0.f), orr[j]);
                 }
             }
             M = mc;

@@ -44,17 +44,25 @@ constexpr int kLayerSpin = 1 << 20;               // bounded barrier wait
 // device-coherent (sc1) accesses, so the barrier needs no cache writeback or
 // invalidate: each wave waits for its own stores to complete, then one lane
 // arrives and waits for the others.
-__device__ __forceinline__ void grid_barrier(unsigned* ctr, unsigned n) {
+// Split form: arrive (after this workgroup's stores are complete), do
+// independent work, then wait.
+__device__ __forceinline__ void grid_arrive(unsigned* ctr) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
     __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void grid_wait(unsigned* ctr, unsigned n) {
     if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (int it = 0; it < kLayerSpin; ++it) {
             if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= n) break;
             __builtin_amdgcn_s_sleep(1);
         }
     }
     __syncthreads();
+}
+__device__ __forceinline__ void grid_barrier(unsigned* ctr, unsigned n) {
+    grid_arrive(ctr);
+    grid_wait(ctr, n);
 }
 
 template <typename HT, bool FP8, int D>
@@ -72,9 +80,17 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
         skinny_lds_body<bf16_t, false, false, true, HT, false, true>(P.qkv, RopeEpi{}, cb, 0, lds.s);
         __syncthreads();
     }
-    grid_barrier(&P.bar[0], nwg);
-    // 2. attention step (every workgroup plans the same ragged split; item w)
-    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, w, 0, 0, lds.d);
+    // 2. attention step (every workgroup plans the same ragged split; item w).
+    // The workgroup arrives at barrier 0 first, then plans its item and
+    // fetches its first K/V block (the cache does not depend on phase 1), and
+    // only then waits; a workgroup without an item waits here.
+    grid_arrive(&P.bar[0]);
+    bool passed = false;
+    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, w, 0, 0, lds.d, [&]() {
+        grid_wait(&P.bar[0], nwg);
+        passed = true;
+    });
+    if (!passed) grid_wait(&P.bar[0], nwg);
     grid_barrier(&P.bar[1], nwg);
     if (w == 0 && threadIdx.x == 0) P.bar[0] = 0u;  // every workgroup is past barrier 0
     // 3. output projection + residual
@@ -235,6 +251,10 @@ extern "C" int supersonic_attn_gfx950_decode_layer(
         const char* v = getenv("SUPERSONIC_DECODE_MIN_CHUNK");
         return (v && *v) ? atoi(v) : 128;
     }());
+    p.det = []() {
+        const char* v = getenv("SUPERSONIC_DECODE_DETERMINISTIC");
+        return (v && *v) ? (atoi(v) != 0) : 0;
+    }();
     p.scale_log2 = scale * kLog2e;
     p.fused = 1;
     p.k_new = k_new;

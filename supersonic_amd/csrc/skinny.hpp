@@ -189,6 +189,13 @@ __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const 
     u32x4_v wv[kSkinnySteps];
 #pragma unroll
     for (int j = 0; j < kSkinnySteps; ++j) wv[j] = wload(s0 + j);
+    // RES: the residual element this thread adds in the epilogue, loaded now so
+    // that its round trip overlaps the weight stream (clamped, branch-free)
+    float res_v = 0.f;
+    if constexpr (RES && !ROPE) {
+        const int row = min(tid >> 4, m - 1), c = min(cbs * 16 + (tid & 15), n - 1);
+        res_v = load_f32<OT>(static_cast<const OT*>(p.res), b * p.o_bs + static_cast<int64_t>(row) * n + c);
+    }
 
     // 3. stage the rows in LDS; chunks past the rows go to a dummy slot at the
     // end of the padding.  The padded rows end at m * ldx - 8 = m * k + 8 (m - 1)
@@ -268,7 +275,7 @@ __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const 
                 for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][tid];
                 float y = bf16_round(sum);
                 const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * n + c;
-                if constexpr (RES) y = bf16_round(load_f32<OT>(static_cast<const OT*>(p.res), o) + y);
+                if constexpr (RES) y = bf16_round(res_v + y);
                 if constexpr (COH_OUT) store_f32_agent<OT>(static_cast<OT*>(pick3(p.out, seg)), o, y);
                 else store_f32<OT>(static_cast<OT*>(pick3(p.out, seg)), o, y);
             }

@@ -98,6 +98,23 @@ def test_decode_eager_runs_agree_to_ulps():
     assert_close_ulps(outs[1], outs[0], "eager repeat", floor=2.0 ** -8)
 
 
+def test_decode_deterministic_runs_are_identical(monkeypatch):
+    """SUPERSONIC_DECODE_DETERMINISTIC=1: a static block order, so two eager
+    runs of the same step give the same bits."""
+    announce("decode deterministic repeat")
+    monkeypatch.setenv("SUPERSONIC_DECODE_DETERMINISTIC", "1")
+    s = torch.cuda.Stream()
+    layer, hidden, hidden0, attn = make_layer(8, 16, 4, 256, 64, 4096, 4000, 94, s)
+    outs = []
+    for _ in range(3):
+        hidden.copy_(hidden0)
+        with torch.cuda.stream(s):
+            layer()
+        s.synchronize()
+        outs.append(attn.clone())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 def test_prefill_graph_replays_match_eager():
     announce("prefill graph")
     S, Hq, Hkv, D, rot, start = 300, 16, 4, 256, 64, 200
