@@ -105,7 +105,7 @@ def main():
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
         out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "prefill_fp8", "fp8", "mixed",
-                                                          "qkv", "qkv_rope", "oproj", "layer_graph")}
+                                                          "qkv", "qkv_rope", "oproj", "proj_gemm", "layer_graph")}
     print(json.dumps(out))
 
 
@@ -378,6 +378,45 @@ class Workloads:
                              "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic("oproj"),
                              "kernel": "skinny_lds_kernel",
                              "bytes_per_launch": kern_bytes}}
+
+    def proj_gemm(self):
+        """Prefill-sized projections on the hand-written MFMA GEMM, config 3's
+        chunk (4096 rows, hidden 4096, 16/4 heads of 256): input norm + Q/K/V
+        (one GEMM, three column segments) and o_proj + residual (the residual
+        add in the GEMM epilogue).  The same calls routed to hipBLASLt
+        (SUPERSONIC_PROJ_GEMM=hipblaslt) are timed alongside for comparison."""
+        import os
+        torch, K = self.torch, self.K
+        rows, hid, nq, nkv, adim = 4096, 4096, 8192, 1024, 4096
+        hidden = self.randn(rows, hid, seed=50)
+        nw = (self.randn(hid, seed=51) * 0.1).to(torch.bfloat16)
+        wq, wk, wv = ((self.randn(n, hid, seed=52 + i) * hid ** -0.5).to(torch.bfloat16).contiguous()
+                      for i, n in enumerate((nq, nkv, nkv)))
+        wo = (self.randn(hid, adim, seed=55) * adim ** -0.5).to(torch.bfloat16).contiguous()
+        attn = self.randn(rows, adim, seed=56)
+        outs = [torch.empty(rows, n, dtype=torch.bfloat16, device=self.dev) for n in (nq, nkv, nkv)]
+        qkv_flops = 2.0 * rows * hid * (nq + 2 * nkv)
+        o_flops = 2.0 * rows * adim * hid
+        res = {"workload": "prefill projections, 4096 rows: norm + Q/K/V 4096 -> 8192 + 2x1024 and "
+                           "o_proj 4096 -> 4096 + residual, bf16"}
+        for label, env in (("", None), ("hipblaslt_", "hipblaslt")):
+            if env:
+                os.environ["SUPERSONIC_PROJ_GEMM"] = env
+            try:
+                _, q_ms, _ = self.timed(lambda i: K.qkv_proj(0, hidden, nw, wq, wk, wv, *outs))
+                h = hidden.clone()
+                _, o_ms, _ = self.timed(lambda i: K.o_proj_residual(0, attn, wo, h))
+            finally:
+                os.environ.pop("SUPERSONIC_PROJ_GEMM", None)
+            res[label + "qkv_ms"] = q_ms
+            res[label + "qkv_tflops"] = qkv_flops / (q_ms * 1e-3) / 1e12
+            res[label + "oproj_ms"] = o_ms
+            res[label + "oproj_tflops"] = o_flops / (o_ms * 1e-3) / 1e12
+        ach = o_flops / (res["oproj_ms"] * 1e-3) / 1e12
+        res["roofline"] = {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                           "kernel": "gemm_bt_kernel (o_proj + residual epilogue)"}
+        return res
 
     def qkv(self):
         """Input norm + Q/K/V projections of a config-2 decode step: 8 rows,

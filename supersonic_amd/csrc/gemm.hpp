@@ -1,0 +1,32 @@
+// Hand-written bf16 GEMM with a transposed right-hand side for the
+// prefill-sized projections: out[m][n] = a[m][k] . w[n][k]^T, fp32
+// accumulation, up to three column segments (separate weights and outputs) in
+// one launch, optionally batched, with a plain bf16 store or a residual add
+// in the epilogue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ssa {
+
+enum GemmEpilogue { kGemmStore = 0, kGemmResidualBf16 = 1, kGemmResidualF32 = 2 };
+
+struct GemmArgs {
+    int batch = 1, m = 0, k = 0;
+    const uint16_t* a = nullptr;  // [batch][m][lda]
+    int64_t lda = 0, a_bs = 0;
+    int nseg = 1;
+    const uint16_t* w[3] = {nullptr, nullptr, nullptr};  // [n_s][k] per segment
+    void* out[3] = {nullptr, nullptr, nullptr};          // [m][n_s] per segment
+    int n[3] = {0, 0, 0};
+    int64_t w_bs = 0, o_bs = 0;  // batch strides (elements) of w and out (segment 0 only when batched)
+    int epilogue = kGemmStore;   // residual: out = bf16(out + bf16(a.w^T)), in place (one segment)
+};
+
+// Launches on `st`; 0 on success.  Requires k % 8 == 0 and 16-byte aligned
+// rows (lda % 8 == 0).
+int gemm_bt(hipStream_t st, const GemmArgs& g);
+
+}  // namespace ssa

@@ -32,6 +32,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <map>
 #include <mutex>
@@ -40,6 +41,7 @@
 #include "common.hpp"
 #include "kv_view.hpp"
 #include "skinny.hpp"
+#include "gemm.hpp"
 #include "supersonic_attn.h"
 
 namespace ssa {
@@ -476,6 +478,30 @@ struct LtDevice {
 std::mutex g_lt_mutex;
 std::map<int, LtDevice> g_lt;
 constexpr size_t kLtWorkspace = 32u << 20;
+// SUPERSONIC_PROJ_GEMM=hipblaslt routes the GEMM-sized projections to
+// hipBLASLt instead of the hand-written kernel (for comparison).
+bool use_hipblaslt() {
+    const char* v = getenv("SUPERSONIC_PROJ_GEMM");
+    return v && std::strcmp(v, "hipblaslt") == 0;
+}
+size_t lt_ws_bytes() { return use_hipblaslt() ? kLtWorkspace : 0; }
+// The three projections (or one) as one hand-written GEMM launch.
+int gemm_segments(hipStream_t st, int m, int k, const void* a, int nseg, const void* const* w, void* const* out,
+                  const int* n, int epilogue = kGemmStore) {
+    GemmArgs g;
+    g.m = m;
+    g.k = k;
+    g.a = static_cast<const uint16_t*>(a);
+    g.lda = k;
+    g.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        g.w[i] = static_cast<const uint16_t*>(w[i]);
+        g.out[i] = out[i];
+        g.n[i] = n[i];
+    }
+    g.epilogue = epilogue;
+    return gemm_bt(st, g);
+}
 
 bool make_layout(hipblasLtMatrixLayout_t* l, uint64_t rows, uint64_t cols, int64_t ld, int batch, int64_t stride) {
     if (hipblasLtMatrixLayoutCreate(l, HIP_R_16BF, rows, cols, ld) != HIPBLAS_STATUS_SUCCESS) return false;
@@ -568,8 +594,22 @@ extern "C" int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(int dtype, s
             } else if (launch_skinny<bf16_t, false>(dev, nullptr, batch, p) != 0) {
                 return 270;  // the reference's launch-failure code covers a workspace failure too
             }
-        } else if (lt_gemm(dev, nullptr, batch, m, n, k, lhs, rhs, out) != 0) {
-            return 270;
+        } else if (use_hipblaslt()) {
+            if (lt_gemm(dev, nullptr, batch, m, n, k, lhs, rhs, out) != 0) return 270;
+        } else {
+            GemmArgs g;
+            g.batch = batch;
+            g.m = m;
+            g.k = k;
+            g.a = static_cast<const uint16_t*>(lhs);
+            g.lda = k;
+            g.a_bs = static_cast<int64_t>(m) * k;
+            g.w[0] = static_cast<const uint16_t*>(rhs);
+            g.out[0] = out;
+            g.n[0] = n;
+            g.w_bs = static_cast<int64_t>(n) * k;
+            g.o_bs = static_cast<int64_t>(m) * n;
+            if (gemm_bt(nullptr, g) != 0) return 270;
         }
     }
     if (hipDeviceSynchronize() != hipSuccess) return 271;
@@ -612,6 +652,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 // the hipBLASLt workspace.
 size_t o_proj_ws_bytes(int m, int n, int k) {
     if (m <= skinny_max_m()) return skinny_ws_bytes(m, k, (n + kSkinnyCols - 1) / kSkinnyCols);
+    if (!use_hipblaslt()) return 256;  // the GEMM adds into the hidden rows in place
     return align256(static_cast<size_t>(m) * n * 2) + kLtWorkspace;
 }
 // Workspace of the qkv entry point: the normed rows, then the streaming
@@ -619,7 +660,7 @@ size_t o_proj_ws_bytes(int m, int n, int k) {
 size_t qkv_ws_bytes(int m, int k, int nq, int nkv) {
     const size_t normed = align256(static_cast<size_t>(m) * k * 2);
     if (m <= skinny_max_m()) return normed + skinny_ws_bytes(m, k, nq / kSkinnyCols + 2 * (nkv / kSkinnyCols));
-    return normed + kLtWorkspace;
+    return normed + lt_ws_bytes();
 }
 }  // namespace ssa
 
@@ -669,6 +710,13 @@ extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, voi
             rc = f32 ? launch_skinny<float, true>(dev, st, 1, p, ws, workspace_bytes)
                      : launch_skinny<bf16_t, true>(dev, st, 1, p, ws, workspace_bytes);
         if (rc) return rc;
+    } else if (!use_hipblaslt()) {
+        if (k == 0) return 0;  // nothing to add
+        const void* w1[1] = {o_proj_w};
+        void* o1[1] = {hidden};
+        const int n1[1] = {n};
+        if (gemm_segments(st, m, k, attn, 1, w1, o1, n1, f32 ? kGemmResidualF32 : kGemmResidualBf16) != 0)
+            return SUPERSONIC_ERR_LAUNCH;
     } else {
         const size_t total = rows * hidden_dim;
         void* y;
@@ -774,14 +822,18 @@ extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stre
             if (rc) return rc;
         }
     } else {
-        // GEMM-sized: one hipBLASLt GEMM per matrix
-        if (ws && rest_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
+        // GEMM-sized: the three matrices as column segments of one GEMM
         const void* wts[3] = {q_proj_w, k_proj_w, v_proj_w};
         void* os[3] = {q_proj_out, k_out, v_out};
         const int ns[3] = {nq, nkv, nkv};
-        for (int i = 0; i < 3; ++i) {
-            if (ns[i] == 0) continue;
-            if (lt_gemm(dev, st, 1, m, ns[i], k, normed, wts[i], os[i], rest) != 0) return SUPERSONIC_ERR_LAUNCH;
+        if (!use_hipblaslt()) {
+            if (gemm_segments(st, m, k, normed, 3, wts, os, ns) != 0) return SUPERSONIC_ERR_LAUNCH;
+        } else {
+            if (ws && rest_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
+            for (int i = 0; i < 3; ++i) {
+                if (ns[i] == 0) continue;
+                if (lt_gemm(dev, st, 1, m, ns[i], k, normed, wts[i], os[i], rest) != 0) return SUPERSONIC_ERR_LAUNCH;
+            }
         }
     }
     if (ev.after) (void)hipEventRecord(ev.after, st);
@@ -936,10 +988,14 @@ extern "C" int supersonic_attn_gfx950_qkv_proj_rope(
             const void* wts[3] = {q_proj_w, k_proj_w, v_proj_w};
             void* os[3] = {qp, kr, vr};
             const int ns[3] = {nq, nkv, nkv};
-            if (workspace && pws_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
-            for (int i = 0; i < 3; ++i)
-                if (lt_gemm(dev, st, 1, m, ns[i], k, normed, wts[i], os[i], workspace ? pws : nullptr) != 0)
-                    return SUPERSONIC_ERR_LAUNCH;
+            if (!use_hipblaslt()) {
+                if (gemm_segments(st, m, k, normed, 3, wts, os, ns) != 0) return SUPERSONIC_ERR_LAUNCH;
+            } else {
+                if (workspace && pws_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
+                for (int i = 0; i < 3; ++i)
+                    if (lt_gemm(dev, st, 1, m, ns[i], k, normed, wts[i], os[i], workspace ? pws : nullptr) != 0)
+                        return SUPERSONIC_ERR_LAUNCH;
+            }
         }
         hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(m, Hq + Hkv), dim3(64), 0, st, qp, kr, vr, e);
         if (hipGetLastError() != hipSuccess) return SUPERSONIC_ERR_LAUNCH;
