@@ -771,7 +771,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // load for their (M, L) (lane c holds split c's) and one per split for the
     // dims, polled until no word reads zero; each word read is then set back
     // to zero for the next call.  The gate goes out with the first round.
-    constexpr int MCH = 16;
+    constexpr int MCH = 16;  // splits a round (32 measured slower: the merge then spills)
     const int WPH = 2 * G <= NW ? 2 : 1;                 // waves per head
     const int part = WPH == 2 ? wave % 2 : 0;
     const int half = WPH == 2 ? (ns + 1) / 2 : ns;
@@ -873,6 +873,16 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 }
             }
             const int64_t ob = (static_cast<int64_t>(b) * p.Hq + h) * D + lane * DV;
+            uint16_t* const op = reinterpret_cast<uint16_t*>(static_cast<QT*>(p.out)) + ob;
+            if constexpr (DV == 4) {
+                if ((reinterpret_cast<uintptr_t>(op) & 7) == 0) {  // one 8-byte store of the lane's 4 dims
+                    const uint64_t v = static_cast<uint64_t>(pack2<QT>(r[0], r[1])) |
+                                       (static_cast<uint64_t>(pack2<QT>(r[2], r[3])) << 32);
+                    if constexpr (COH) __hip_atomic_store(reinterpret_cast<uint64_t*>(op), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else *reinterpret_cast<uint64_t*>(op) = v;
+                    return;
+                }
+            }
 #pragma unroll
             for (int j = 0; j < DV; ++j) {
                 if constexpr (COH) store_f32_agent(static_cast<QT*>(p.out), ob + j, r[j]);
