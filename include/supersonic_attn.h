@@ -185,9 +185,10 @@ typedef struct supersonic_kv_cache {
 
 /* Bytes of workspace supersonic_attn_gfx950_decode needs for this shape.
  * A caller-owned workspace must be zero-filled before its first use and not
- * written by the caller between calls: it holds per-(sequence, kv head)
- * split counters and the split partials (a zero word marks a partial not yet
- * written), all of which every call leaves at zero.  Calls that share a
+ * written by the caller between calls: its first 64 KiB hold per-(sequence,
+ * kv head) split counters that every call leaves at zero, the rest the split
+ * partials (a zero word marks a partial not yet written; each split zeroes its
+ * own slots before it writes them).  Calls that share a
  * workspace must not overlap.  batch * kv_heads <= 16384. */
 size_t supersonic_attn_gfx950_decode_workspace_size(
     size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t max_kv_len);

@@ -277,6 +277,22 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     const int G = p.G;
     const int pos = len - 1;
     const bool owner = p.fused && pos >= t_begin && pos < t_end;
+    // This split's partial slots go to zero before any of its loads is
+    // issued: a slot may still hold a partial of an earlier call, and the
+    // merge polls for non-zero words.  A wave waits for its own row loads
+    // (issued after these stores; vmcnt drains in issue order) before the
+    // split can arrive, so the zeros have landed by then.  Wave hh owns head
+    // row hh (the wave that stores the partial later), wave 0 the (M, L) words.
+    {
+        constexpr int DVz = D / 64;
+        for (int hh = wave; hh < G; hh += NW)
+            st_coh<DVz>(p.part_o + (pre_b * p.Hq + static_cast<int64_t>(kvh * G + hh) * n_b + split) * D,
+                        lane * DVz * 4, typename U32N<DVz>::t{});
+        if (wave == 0 && lane < G)
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(
+                                   &p.part_ml[2 * (pre_b * p.Hq + static_cast<int64_t>(kvh * G + lane) * n_b + split)]),
+                               uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     const int n_s = lane & 15;           // score lane: token within the block
     const int vt = lane / LPT;           // V lane: token within the instruction
@@ -769,8 +785,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // many waves as heads, two waves share a head, each taking half of the
     // splits, and combine through LDS.  A wave takes MCH splits a round: one
     // load for their (M, L) (lane c holds split c's) and one per split for the
-    // dims, polled until no word reads zero; each word read is then set back
-    // to zero for the next call.  The gate goes out with the first round.
+    // dims, polled until no word reads zero (every split zeroed its own slots
+    // as it started).  The gate goes out with the first round.
     constexpr int MCH = 16;  // splits a round (32 measured slower: the merge then spills)
     const int WPH = 2 * G <= NW ? 2 : 1;                 // waves per head
     const int part = WPH == 2 ? wave % 2 : 0;
@@ -889,18 +905,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 else store_f32(static_cast<QT*>(p.out), ob + j, r[j]);
             }
         };
-        // the words read go back to zero (this split's own row was never
-        // stored); after the rounds, so that no load of a later round waits
-        // behind these stores
-        auto reset = [&]() {
-            for (int s1 = sp_lo; s1 < sp_hi; s1 += 64)
-                if (s1 + lane < sp_hi && s1 + lane != split) st_coh<2>(pml, 8 * (s1 + lane), u32x2_v{0u, 0u});
-            for (int s1 = sp_lo; s1 < sp_hi; ++s1)
-                if (s1 != split) st_coh<DV>(po + static_cast<int64_t>(s1) * D, lane * DV * 4, dv_t{});
-        };
         if (WPH == 1) {
             finish();
-            reset();
         } else {
             // two waves per head: the second parks (M, L, o) in LDS (smem is
             // free once every wave has read its own partial), the first
@@ -925,7 +931,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 for (int j = 0; j < DV; ++j) orr[j] = orr[j] * a1 + park[lane * DV + j] * a2;
                 finish();
             }
-            reset();
         }
     }
     if (WPH == 2 && my_h < 0) {  // waves without a head still take part in the two barriers

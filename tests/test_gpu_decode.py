@@ -195,7 +195,9 @@ def test_decode_attend_ragged_with_empty_sequences():
 
 def test_fused_decode_caller_workspace_reuse():
     """A zero-filled caller workspace serves consecutive calls of different
-    shapes (the split counters and partial slots are left at zero)."""
+    shapes: the split counters are left at zero, and a partial slot left by an
+    earlier call (the shapes here reuse slots with other meanings) is zeroed by
+    the split that owns it in the next call before the merge can read it."""
     announce("fused decode caller workspace reuse")
     n = max(K.decode_workspace_size(4, 16, 4, 256, 4097), K.decode_workspace_size(2, 8, 2, 128, 2049))
     ws = torch.zeros(n, dtype=torch.uint8, device=DEV)
@@ -206,7 +208,7 @@ def test_fused_decode_caller_workspace_reuse():
         out, _ = run_fused(case, workspace=ws)
         ref, _, _, _, _ = oracle_decode(case)
         check(out, ref, TOL_BF16, f"workspace reuse {seed}")
-        assert int(ws.count_nonzero()) == 0
+        assert int(ws[:65536].count_nonzero()) == 0
 
 
 # [256]: chunks of 128 tokens, so the owner split holds only the new token
