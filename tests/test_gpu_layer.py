@@ -19,10 +19,12 @@ from supersonic_amd import kernel_ffi as K
 pytestmark = pytest.mark.gpu
 
 
-def layer_case(seed, B, Hq, Hkv, D, rot, hid, lens, fp8=False, hidden_f32=False):
+def layer_case(seed, B, Hq, Hkv, D, rot, hid, lens, fp8=False, hidden_f32=False, page=None):
     g = gen(seed)
     cap = max(lens) + 1
-    c = dict(B=B, Hq=Hq, Hkv=Hkv, D=D, rot=rot, hid=hid, lens=lens, fp8=fp8)
+    if page:
+        cap = (cap + page - 1) // page * page
+    c = dict(B=B, Hq=Hq, Hkv=Hkv, D=D, rot=rot, hid=hid, lens=lens, fp8=fp8, page=page)
     c["hidden"] = O.randn_bf16(g, B, hid)
     c["nw"] = O.randn_bf16(g, hid, std=0.1)
     c["wq"], c["wk"], c["wv"] = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (Hq * 2 * D, Hkv * D, Hkv * D))
@@ -40,8 +42,36 @@ def layer_case(seed, B, Hq, Hkv, D, rot, hid, lens, fp8=False, hidden_f32=False)
     return c
 
 
+def paged(c):
+    """The contiguous cache of case c as a pool of pages in a shuffled order plus a block table."""
+    ps, B, Hkv = c["page"], c["B"], c["Hkv"]
+    per = c["k"].shape[2] // ps
+    perm = torch.randperm(B * per, generator=gen(7))
+    def pool(t):
+        if t is None:
+            return None
+        out = torch.zeros((B * per, Hkv, ps) + tuple(t.shape[3:]), dtype=t.dtype)
+        for b in range(B):
+            for j in range(per):
+                out[int(perm[b * per + j])] = t[b, :, j * ps:(j + 1) * ps]
+        return out
+    bt = torch.tensor([[int(perm[b * per + j]) for j in range(per)] for b in range(B)], dtype=torch.int32)
+    return pool(c["k"]), pool(c["v"]), pool(c["ks"]), pool(c["vs"]), bt
+
+
+def appended_v(c, cache, b, p):
+    if not c["page"]:
+        return cache.v[b, :, p].cpu()
+    ps = c["page"]
+    return cache.v[int(c["bt"][b, p // ps]), :, p % ps].cpu()
+
+
 def run_layer(c, ws):
-    cache = K.KvCache(dev(c["k"]), dev(c["v"]), dev(c["ks"]), dev(c["vs"]))
+    if c["page"]:
+        k, v, ks, vs, c["bt"] = paged(c)
+        cache = K.KvCache(dev(k), dev(v), dev(ks), dev(vs), block_table=c["bt"].to(DEV))
+    else:
+        cache = K.KvCache(dev(c["k"]), dev(c["v"]), dev(c["ks"]), dev(c["vs"]))
     h = c["hidden"].to(c["hidden_dtype"]).to(DEV)
     pos = torch.tensor(c["lens"], dtype=torch.int32, device=DEV)
     K.decode_layer(0, h, dev(c["nw"]), dev(c["wq"]), dev(c["wk"]), dev(c["wv"]), dev(c["qw"]), dev(c["kw"]),
@@ -73,7 +103,7 @@ def check_layer(c, out, cache, ref, v_ref):
     for b, p in enumerate(c["lens"]):
         # the appended V row is this layer's own projection: within the projection's
         # rounding (fp32 summation order) of the oracle's (fp8: one code)
-        got, want = cache.v[b, :, p].cpu(), v_ref[b, :, p]
+        got, want = appended_v(c, cache, b, p), v_ref[b, :, p]
         if c["fp8"]:
             assert (got.int() - want.int()).abs().max().item() <= 1 or (got != want).float().mean().item() < 0.02
         else:
@@ -89,6 +119,8 @@ CASES = {
     "d128": dict(B=2, Hq=8, Hkv=2, D=128, rot=32, hid=2048, lens=[700, 2100]),
     "fp8": dict(B=2, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[1200, 333], fp8=True),
     "f32_hidden": dict(B=3, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[64, 65, 900], hidden_f32=True),
+    "paged": dict(B=3, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[700, 64, 1500], page=64),
+    "paged_fp8": dict(B=2, Hq=8, Hkv=2, D=128, rot=32, hid=1024, lens=[1000, 129], fp8=True, page=64),
 }
 
 

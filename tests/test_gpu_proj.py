@@ -51,6 +51,9 @@ def test_matmul_known_answer():
     (1, 1, 64, 4096), (1, 8, 4096, 4096), (1, 17, 100, 264), (2, 16, 40, 72), (1, 64, 48, 512),
     (1, 65, 128, 256), (1, 300, 96, 200), (1, 5, 33, 100), (2, 130, 64, 96),
     (2, 8, 4096, 1024), (3, 16, 2048, 2048),  # the LDS-staged kernel with a batch dimension
+    # the tiled GEMM: partial tiles in m, n and k, n not a multiple of 8 (scalar
+    # epilogue), k not a multiple of 8 (the one-thread-per-output kernel), batch
+    (1, 700, 1000, 520), (1, 257, 100, 264), (2, 300, 264, 136), (1, 40, 24, 36), (1, 512, 768, 1024),
 ])
 def test_matmul_matches_oracle(batch, m, n, k):
     announce(f"matmul batch={batch} m={m} n={n} k={k}")
