@@ -110,12 +110,15 @@ struct SkinnyLdsParams {
     int64_t x_bs, w_bs, o_bs;
 };
 
-// LDS of one weight-streaming workgroup.
-struct SkinnyLds {
+// LDS of one weight-streaming workgroup (SkinnyLdsBase without the NORM
+// staging array: 74 KB, so two workgroups share a CU).
+struct SkinnyLdsBase {
     __attribute__((aligned(16))) uint16_t xs[kXsMax + 16 * 8];
     __attribute__((aligned(16))) float red[kSkinnyWaves][256];
-    float part[kXsMax / 8];   // NORM staging: sum of squares of each 8-element chunk
     int last_s;
+};
+struct SkinnyLds : SkinnyLdsBase {
+    float part[kXsMax / 8];   // NORM staging: sum of squares of each 8-element chunk
 };
 
 // One workgroup of the weight stream: column block cb of batch element b.
@@ -124,9 +127,9 @@ struct SkinnyLds {
 // device-coherent accesses (data exchanged with other workgroups of the same
 // kernel).
 template <typename OT, bool RES, bool ROPE, bool NORM = false, typename XT = bf16_t, bool COH_IN = false,
-          bool COH_OUT = false>
+          bool COH_OUT = false, typename LdsT = SkinnyLds>
 __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const RopeEpi& e, int cb, int b,
-                                                SkinnyLds& L) {
+                                                LdsT& L) {
     uint16_t (&xs)[kXsMax + 16 * 8] = L.xs;
     float (&red)[kSkinnyWaves][256] = L.red;
     // opaque: when several bodies are inlined into one kernel, lane-derived
