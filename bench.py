@@ -105,7 +105,7 @@ def main():
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
         out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "prefill_fp8", "fp8", "mixed",
-                                                          "qkv", "qkv_rope", "oproj", "proj_gemm", "layer_graph")}
+                                                          "qkv", "qkv_rope", "oproj", "proj_gemm", "prefill_layer", "layer_graph")}
     print(json.dumps(out))
 
 
@@ -284,6 +284,55 @@ class Workloads:
                 "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
                              "traffic": measured_traffic("prefill"), "kernel": "prefill_kernel"}}
+
+    def prefill_layer(self):
+        """One prefill chunk of a full-attention layer end to end on this
+        library, config 3's shape (4096 tokens, hidden 4096, 16/4 heads of 256):
+        input norm + Q/K/V (hand-written GEMM), the fused attention (QK norm,
+        RoPE, cache append, causal MFMA attention, gate) and o_proj + residual
+        (GEMM with the residual add in its epilogue), back to back on one
+        stream; the whole chunk is timed by events."""
+        torch, K = self.torch, self.K
+        S, hid, Hq, Hkv, D, rot = 4096, 4096, 16, 4, 256, 64
+        hidden = self.randn(S, hid, seed=60)
+        nw = (self.randn(hid, seed=61) * 0.1).to(torch.bfloat16)
+        wq, wk, wv = ((self.randn(n, hid, seed=62 + i) * hid ** -0.5).to(torch.bfloat16).contiguous()
+                      for i, n in enumerate((Hq * 2 * D, Hkv * D, Hkv * D)))
+        wo = (self.randn(hid, Hq * D, seed=65) * (Hq * D) ** -0.5).to(torch.bfloat16).contiguous()
+        q_proj = torch.empty(S, Hq * 2 * D, dtype=torch.bfloat16, device=self.dev)
+        k_new = torch.empty(S, Hkv * D, dtype=torch.bfloat16, device=self.dev)
+        v_new = torch.empty(S, Hkv * D, dtype=torch.bfloat16, device=self.dev)
+        qw = (self.randn(D, seed=66).float() * 0.02 + 1).bfloat16()
+        kw = (self.randn(D, seed=67).float() * 0.02 + 1).bfloat16()
+        cos, sin = (t.to(self.dev) for t in K.rope_tables(rot, S + 1, 1.0e7))
+        cache = K.KvCache(torch.zeros(1, Hkv, S, D, dtype=torch.bfloat16, device=self.dev),
+                          torch.zeros(1, Hkv, S, D, dtype=torch.bfloat16, device=self.dev))
+        attn = torch.empty(S, Hq * D, dtype=torch.bfloat16, device=self.dev)
+        h = hidden.clone()
+        ws = torch.zeros(K.prefill_workspace_size(False, Hkv, D, S, 0), dtype=torch.uint8, device=self.dev)
+
+        def step(i):
+            K.qkv_proj(0, h, nw, wq, wk, wv, q_proj, k_new, v_new)
+            K.fused_prefill(0, q_proj, k_new, v_new, qw, kw, cos, sin, cache, attn, q_heads=Hq, kv_heads=Hkv,
+                            head_dim=D, rotary_dim=rot, chunk_start=0, workspace=ws)
+            K.o_proj_residual(0, attn, wo, h)
+        for _ in range(self.warmup):
+            step(0)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(self.steps):
+            step(0)
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / self.steps
+        proj_fl = 2.0 * S * hid * (Hq * 2 * D + 2 * Hkv * D) + 2.0 * S * Hq * D * hid
+        attn_fl = self.causal_flops(S, Hq, D)
+        return {"workload": "prefill layer, 4096-token chunk: norm + Q/K/V GEMM, fused attention, o_proj GEMM + "
+                            "residual (config 3 shape, hidden 4096)",
+                "ms_per_step": ms, "flops": proj_fl + attn_fl,
+                "tflops": (proj_fl + attn_fl) / (ms * 1e-3) / 1e12,
+                "frac_of_bf16_peak": (proj_fl + attn_fl) / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
 
     def prefill_fp8(self):
         """FP8 (OCP e4m3) KV lane of the fused prefill: a 4096-token chunk after a
