@@ -269,10 +269,12 @@ struct ScopedDevice {
 // prefill V^T staging never share memory.
 constexpr int kWorkspaceDecode = 0;
 constexpr int kWorkspacePrefill = 1;
-constexpr int kWorkspaceProj = 2;    // GEMM output of the large-row o_proj path
+constexpr int kWorkspaceProj = 2;    // scratch rows: the o_proj GEMM output (hipBLASLt path), qkv_proj normed rows
 constexpr int kWorkspaceProjLt = 3;  // hipBLASLt workspace
 constexpr int kWorkspaceSkinny = 4;  // split-k partials and arrival counters of the o_proj kernel
-constexpr int kWorkspaceSlots = 5;
+constexpr int kWorkspaceGemm = 5;    // tail-split partials and flags of the hand-written GEMM
+constexpr int kWorkspaceRope = 6;    // qkv_proj_rope: per-head counters (zero between calls), then rows
+constexpr int kWorkspaceSlots = 7;
 void* device_workspace(int device, size_t bytes, int slot);
 
 // Compute units of `device` (cached; 256 on MI355X), 0 if the query fails.

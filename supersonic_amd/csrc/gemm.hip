@@ -48,6 +48,13 @@ struct GemmKParams {
     int64_t w_bs, o_bs;
     int m, k, mt, nt, tiles;
     int vec_mask;   // bit s: segment s takes 16-byte output chunks
+    // Tail split: the first `full` tiles of the order run whole; each of the
+    // remaining `tail` tiles runs as two workgroups over the two halves of k
+    // (k-tiles [0, khalf) and [khalf, KT)), the first handing its fp32
+    // accumulators to the second through `part` and a flag.
+    int full, tail, khalf;
+    uint32_t* part;      // [tail][8 waves][32][64 lanes] x 16 bytes
+    unsigned* flags;     // [tail], zero between calls
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const uint16_t* base, int64_t bytes) {
@@ -65,12 +72,16 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int b = blockIdx.y;
 
-    // ---- tile of this workgroup (XCD-contiguous ranges of the tile order)
+    // ---- tile of this workgroup (XCD-contiguous ranges of the tile order;
+    // the tail tiles, two workgroups each, follow the whole ones)
     const int i = blockIdx.x;
-    const int T = p.tiles;
+    const int T = p.full;
+    const bool is_tail = i >= T;
+    const int tj = i - T;               // tail: workgroup index within the tail
+    const int half = tj & 1;            // tail: which half of k
     const int q = T / 8, r = T % 8;
     const int xcd = i % 8, slot = i / 8;
-    const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+    const int t = is_tail ? T + (tj >> 1) : (xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot);
     const int band = t / (kGBand * p.nt);
     const int gm = min(kGBand, p.mt - band * kGBand);
     const int tin = t - band * kGBand * p.nt;
@@ -87,6 +98,11 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     const __amdgpu_buffer_rsrc_t ar = gemm_rsrc(abase, static_cast<int64_t>(p.m - m0) * p.lda * 2);
     const __amdgpu_buffer_rsrc_t wr = gemm_rsrc(wbase, static_cast<int64_t>(ns - n0) * k * 2);
 
+    // k-tiles kt0 .. KT-1 of this workgroup; k-tile kt goes to stage
+    // (kt - kt0) % kGStages
+    const int KT_all = (k + kGBK - 1) / kGBK;
+    const int kt0 = is_tail && half ? p.khalf : 0;
+    const int KT = is_tail && !half ? p.khalf : KT_all;
     // ---- direct global->LDS copies: instruction j of a wave moves rows
     // rr = kGCopyRows (kGCopies wave + j) .. of a tile; lane l takes row
     // rr + l / kGCpr and physical chunk l % kGCpr, i.e. the logical chunk
@@ -97,7 +113,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     constexpr int kOOB = 0x7ffffff0;  // offset past any range: reads zero
     auto issue = [&](int kt) {
         const int k0 = kt * kGBK;
-        const int st = kt % kGStages;
+        const int st = (kt - kt0) % kGStages;
         uint8_t* sa = lds + st * kGStageBytes;
         uint8_t* sw = sa + kGTileBytes;
 #pragma unroll
@@ -132,7 +148,6 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     const int a_rd = (wm * 128 + orow) * kGRowB;
     const int w_rd = (wn * 64 + orow) * kGRowB;
 
-    const int KT = (k + kGBK - 1) / kGBK;
     // Wait until tile kt has landed in LDS (this wave's copies, then every
     // wave's through the barrier); tile kt + 3 then goes to the stage of tile
     // kt - 1, which every wave has finished reading.  A wave issues
@@ -148,7 +163,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     };
     // Fragments of k16 step s of tile kt, and the 16 MFMAs of one step.
     auto read_frags = [&](int kt, int s, bf16x8_v (&af)[4], bf16x8_v (&bfr)[2]) {
-        const uint8_t* sa = lds + (kt % kGStages) * kGStageBytes;
+        const uint8_t* sa = lds + ((kt - kt0) % kGStages) * kGStageBytes;
         const uint8_t* sw = sa + kGTileBytes;
         const int ck = (2 * s + (lane >> 5)) ^ sw_x;
 #pragma unroll
@@ -166,17 +181,17 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
                 acc[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ib], bfr[jb], acc[ib][jb], 0, 0, 0);
     };
 #pragma unroll
-    for (int kt = 0; kt < kGStages - 1; ++kt)
-        if (kt < KT) issue(kt);
+    for (int u = 0; u < kGStages - 1; ++u)
+        if (kt0 + u < KT) issue(kt0 + u);
     // Software pipeline over the k16 steps: the fragments of the next step
     // are read while the MFMAs of the current one run (two register sets).
     bf16x8_v a0[4], b0[2], a1[4], b1[2];
-    if (KT > 0) {
-        arrive_tile(0);
-        read_frags(0, 0, a0, b0);
+    if (kt0 < KT) {
+        arrive_tile(kt0);
+        read_frags(kt0, 0, a0, b0);
     }
     constexpr int NS = kGBK / 16;  // k16 steps a tile (even)
-    for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = kt0; kt < KT; ++kt) {
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             bf16x8_v(&ca)[4] = (st & 1) ? a1 : a0;
@@ -191,6 +206,53 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
             }
             mma_step(ca, cb);
         }
+    }
+
+    // ---- tail hand-over: the first half stores its accumulators
+    // (device-coherent 16-byte stores, lane-contiguous) and, once every
+    // wave's stores have completed, raises the tile's flag; the second half
+    // waits for the flag (bounded: both halves run in the same last round of
+    // workgroups) and adds them.
+    if (is_tail) {
+        uint32_t* pt = p.part + ((static_cast<int64_t>(tj >> 1) * 8 + wave) * 32) * 64 * 4;
+        unsigned* flag = p.flags + (tj >> 1);
+        if (!half) {
+#pragma unroll
+            for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+                for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+                    for (int qd = 0; qd < 4; ++qd) {
+                        const int rr = (ib * 2 + jb) * 4 + qd;
+                        u32x4_v v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = __float_as_uint(acc[ib][jb][4 * qd + e]);
+                        st_coh<4>(pt + rr * 64 * 4, lane * 16, v);
+                    }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        if (tid == 0) {
+            for (int it = 0; it < (1 << 22); ++it) {
+                if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+            __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    const int rr = (ib * 2 + jb) * 4 + qd;
+                    const u32x4_v v = ld_coh<4>(pt + rr * 64 * 4, lane * 16);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[ib][jb][4 * qd + e] += __uint_as_float(v[e]);
+                }
     }
 
     // ---- epilogue, through LDS: lane holds column wn 64 + jb 32 + lane % 32
@@ -328,6 +390,24 @@ int gemm_bt(hipStream_t st, const GemmArgs& g) {
     const int64_t tiles = static_cast<int64_t>(p.mt) * nt;
     if (tiles > 0x7fffffff) return 1;
     p.tiles = static_cast<int>(tiles);
+    p.full = p.tiles;
+    {
+        // Tail split: with whole rounds of one workgroup a CU, the last
+        // partial round's tiles run as two half-k workgroups each.
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        const int cus = device_cu_count(dev) > 0 ? device_cu_count(dev) : 256;
+        const int tail = p.tiles % cus;
+        const int KT = (g.k + kGBK - 1) / kGBK;
+        if (g.batch == 1 && p.tiles > cus && tail > 0 && 2 * tail <= cus && KT >= 4 &&
+            g.ws && g.ws_bytes >= gemm_tail_bytes(tail)) {
+            p.full = p.tiles - tail;
+            p.tail = tail;
+            p.khalf = KT / 2;
+            p.flags = static_cast<unsigned*>(g.ws);
+            p.part = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(g.ws) + kGemmFlagBytes);
+        }
+    }
     if (!tiled) {
         const int64_t total = static_cast<int64_t>(g.m) * (p.n[0] + p.n[1] + p.n[2]);
         const dim3 sgrid(static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536)),
@@ -339,7 +419,7 @@ int gemm_bt(hipStream_t st, const GemmArgs& g) {
         }
         return hipGetLastError() == hipSuccess ? 0 : 1;
     }
-    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(g.batch)), blk(kGThreads);
+    const dim3 grid(static_cast<unsigned>(p.full + 2 * p.tail), static_cast<unsigned>(g.batch)), blk(kGThreads);
     switch (g.epilogue) {
     case kGemmResidualBf16: hipLaunchKernelGGL(gemm_bt_kernel<kGemmResidualBf16>, grid, blk, 0, st, p); break;
     case kGemmResidualF32: hipLaunchKernelGGL(gemm_bt_kernel<kGemmResidualF32>, grid, blk, 0, st, p); break;

@@ -23,7 +23,26 @@ struct GemmArgs {
     int n[3] = {0, 0, 0};
     int64_t w_bs = 0, o_bs = 0;  // batch strides (elements) of w and out (segment 0 only when batched)
     int epilogue = kGemmStore;   // residual: out = bf16(out + bf16(a.w^T)), in place (one segment)
+    // Optional workspace (zero-filled before its first use; every call leaves
+    // its flags at zero) for splitting the last partial round of tiles along
+    // k; without one (or too small) the tail runs whole.
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
 };
+
+constexpr size_t kGemmFlagBytes = 4096;  // tail flags (<= 1024 tail tiles)
+// Workspace bytes of the tail split for `tail` tiles.
+inline size_t gemm_tail_bytes(int tail) { return kGemmFlagBytes + static_cast<size_t>(tail) * 8 * 32 * 64 * 16; }
+// Workspace bytes for the tail split of a GEMM of m rows and the given
+// column segments on a GPU of `cus` CUs (256 on MI355X); 0 when it has no
+// tail to split.
+inline size_t gemm_ws_bytes(int m, int nseg, const int* n, int cus = 256) {
+    int64_t nt = 0;
+    for (int s = 0; s < nseg; ++s) nt += (n[s] + 255) / 256;
+    const int64_t tiles = static_cast<int64_t>((m + 255) / 256) * nt;
+    const int tail = static_cast<int>(tiles % cus);
+    return tiles > cus && tail > 0 && 2 * tail <= cus ? gemm_tail_bytes(tail) : 0;
+}
 
 // Launches on `st`; 0 on success.  Requires k % 8 == 0 and 16-byte aligned
 // rows (lda % 8 == 0).

@@ -485,9 +485,11 @@ bool use_hipblaslt() {
     return v && std::strcmp(v, "hipblaslt") == 0;
 }
 size_t lt_ws_bytes() { return use_hipblaslt() ? kLtWorkspace : 0; }
-// The three projections (or one) as one hand-written GEMM launch.
-int gemm_segments(hipStream_t st, int m, int k, const void* a, int nseg, const void* const* w, void* const* out,
-                  const int* n, int epilogue = kGemmStore) {
+// The three projections (or one) as one hand-written GEMM launch.  ws: the
+// caller's region for the tail split (gemm_ws_bytes()), or null for the
+// library's own.
+int gemm_segments(int dev, hipStream_t st, int m, int k, const void* a, int nseg, const void* const* w,
+                  void* const* out, const int* n, int epilogue, uint8_t* ws, size_t ws_bytes) {
     GemmArgs g;
     g.m = m;
     g.k = k;
@@ -500,6 +502,16 @@ int gemm_segments(hipStream_t st, int m, int k, const void* a, int nseg, const v
         g.n[i] = n[i];
     }
     g.epilogue = epilogue;
+    const size_t need = gemm_ws_bytes(m, nseg, n);
+    if (need > 0) {
+        if (ws) {
+            if (ws_bytes < need) return 1;
+            g.ws = ws;
+        } else {
+            g.ws = device_workspace(dev, need, kWorkspaceGemm);  // zero-filled once; flags stay zero after a call
+        }
+        g.ws_bytes = g.ws ? need : 0;
+    }
     return gemm_bt(st, g);
 }
 
@@ -609,6 +621,11 @@ extern "C" int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(int dtype, s
             g.n[0] = n;
             g.w_bs = static_cast<int64_t>(n) * k;
             g.o_bs = static_cast<int64_t>(m) * n;
+            if (batch == 1) {
+                g.ws_bytes = gemm_ws_bytes(m, 1, &n);
+                if (g.ws_bytes > 0) g.ws = device_workspace(dev, g.ws_bytes, kWorkspaceGemm);
+                if (!g.ws) g.ws_bytes = 0;
+            }
             if (gemm_bt(nullptr, g) != 0) return 270;
         }
     }
@@ -652,7 +669,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 // the hipBLASLt workspace.
 size_t o_proj_ws_bytes(int m, int n, int k) {
     if (m <= skinny_max_m()) return skinny_ws_bytes(m, k, (n + kSkinnyCols - 1) / kSkinnyCols);
-    if (!use_hipblaslt()) return 256;  // the GEMM adds into the hidden rows in place
+    if (!use_hipblaslt()) return 256 + gemm_ws_bytes(m, 1, &n);  // the GEMM adds into the hidden rows in place
     return align256(static_cast<size_t>(m) * n * 2) + kLtWorkspace;
 }
 // Workspace of the qkv entry point: the normed rows, then the streaming
@@ -660,7 +677,8 @@ size_t o_proj_ws_bytes(int m, int n, int k) {
 size_t qkv_ws_bytes(int m, int k, int nq, int nkv) {
     const size_t normed = align256(static_cast<size_t>(m) * k * 2);
     if (m <= skinny_max_m()) return normed + skinny_ws_bytes(m, k, nq / kSkinnyCols + 2 * (nkv / kSkinnyCols));
-    return normed + lt_ws_bytes();
+    const int ns[3] = {nq, nkv, nkv};
+    return normed + (use_hipblaslt() ? lt_ws_bytes() : gemm_ws_bytes(m, 3, ns));
 }
 }  // namespace ssa
 
@@ -715,7 +733,8 @@ extern "C" int supersonic_attn_gfx950_o_proj_residual(size_t device_ordinal, voi
         const void* w1[1] = {o_proj_w};
         void* o1[1] = {hidden};
         const int n1[1] = {n};
-        if (gemm_segments(st, m, k, attn, 1, w1, o1, n1, f32 ? kGemmResidualF32 : kGemmResidualBf16) != 0)
+        if (gemm_segments(dev, st, m, k, attn, 1, w1, o1, n1, f32 ? kGemmResidualF32 : kGemmResidualBf16, ws,
+                          workspace_bytes) != 0)
             return SUPERSONIC_ERR_LAUNCH;
     } else {
         const size_t total = rows * hidden_dim;
@@ -827,7 +846,8 @@ extern "C" int supersonic_attn_gfx950_qkv_proj(size_t device_ordinal, void* stre
         void* os[3] = {q_proj_out, k_out, v_out};
         const int ns[3] = {nq, nkv, nkv};
         if (!use_hipblaslt()) {
-            if (gemm_segments(st, m, k, normed, 3, wts, os, ns) != 0) return SUPERSONIC_ERR_LAUNCH;
+            if (gemm_segments(dev, st, m, k, normed, 3, wts, os, ns, kGemmStore, ws ? rest : nullptr, rest_bytes) != 0)
+                return SUPERSONIC_ERR_LAUNCH;
         } else {
             if (ws && rest_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
             for (int i = 0; i < 3; ++i) {
@@ -901,7 +921,7 @@ extern "C" int supersonic_attn_gfx950_qkv_proj_rope(
         if (workspace_bytes < need) return SUPERSONIC_ERR_WORKSPACE;
     } else {
         // zero-filled once; every call leaves the counters at zero
-        ws = static_cast<uint8_t*>(device_workspace(dev, need, kWorkspaceProj));
+        ws = static_cast<uint8_t*>(device_workspace(dev, need, kWorkspaceRope));
         if (!ws) return SUPERSONIC_ERR_WORKSPACE;
     }
     RopeEpi e{};
@@ -989,7 +1009,9 @@ extern "C" int supersonic_attn_gfx950_qkv_proj_rope(
             void* os[3] = {qp, kr, vr};
             const int ns[3] = {nq, nkv, nkv};
             if (!use_hipblaslt()) {
-                if (gemm_segments(st, m, k, normed, 3, wts, os, ns) != 0) return SUPERSONIC_ERR_LAUNCH;
+                if (gemm_segments(dev, st, m, k, normed, 3, wts, os, ns, kGemmStore, workspace ? pws : nullptr,
+                                  pws_bytes) != 0)
+                    return SUPERSONIC_ERR_LAUNCH;
             } else {
                 if (workspace && pws_bytes < kLtWorkspace) return SUPERSONIC_ERR_WORKSPACE;
                 for (int i = 0; i < 3; ++i)

@@ -65,6 +65,21 @@ def test_matmul_matches_oracle(batch, m, n, k):
     assert_ulps(out, ref, ulp(ref) + 1e-6, "matmul")
 
 
+def test_matmul_tail_split():
+    """More tiles than CUs with a short last round: the tail tiles run as two
+    half-k workgroups whose fp32 partials meet through the workspace.  Two calls
+    in a row (the second of another shape and tail) check that each call leaves
+    the hand-over flags cleared; the partial last k-tile sits in the second half."""
+    for seed, (m, n, k) in enumerate([(4096, 4608, 512), (4100, 4608, 520), (4096, 4608, 512)]):
+        announce(f"matmul tail split m={m} n={n} k={k}")
+        g = gen(90 + seed)
+        lhs = O.randn_bf16(g, 1, m, k)
+        rhs = O.randn_bf16(g, 1, n, k, std=k ** -0.5)
+        out = dropin_matmul(lhs, rhs)
+        ref = O.matmul_rhs_transposed(lhs, rhs)
+        assert_ulps(out, ref, ulp(ref) + 1e-6, f"matmul tail split {m}x{n}x{k}")
+
+
 @pytest.mark.parametrize("m,k", [(12, 2728), (15, 2184), (16, 2048)])
 def test_matmul_lds_staging_padded_rows(m, k, monkeypatch):
     """The LDS-staged kernel with rows whose padded end, m * k + 8 (m - 1), passes
@@ -222,6 +237,36 @@ def test_qkv_proj_matches_oracle(rows, hid, nq, nkv, hdt):
         # (hardware rsqrt), which moves a projection by far less than its ulp
         assert_ulps(out, ref, 2 * ulp(ref) + 2.0 ** -10, f"qkv {name}")
         assert (out.float() == ref).float().mean().item() > 0.9, name
+
+
+@pytest.mark.parametrize("caller_ws", [False, True])
+def test_qkv_proj_gemm_tail_split(caller_ws):
+    """A prefill-sized Q/K/V: 640 GEMM tiles, the last 128 split along k, with
+    the library's workspace or the caller's (zero-filled once, reused)."""
+    rows, hid, nq, nkv = 4096, 1024, 8192, 1024
+    announce(f"qkv_proj tail split rows={rows} caller workspace {caller_ws}")
+    g = gen(87)
+    hidden = O.randn_bf16(g, rows, hid)
+    nw = O.randn_bf16(g, hid, std=0.1)
+    wq, wk, wv = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (nq, nkv, nkv))
+    ws = None
+    if caller_ws:
+        ws = torch.zeros(K.qkv_proj_workspace_size(rows, hid, nq, nkv), dtype=torch.uint8, device=DEV)
+    refs = O.qkv_proj(hidden.float(), nw, wq, wk, wv)
+    for _ in range(2):
+        outs = [torch.full((rows, w.shape[0]), float("nan"), dtype=torch.bfloat16, device=DEV) for w in (wq, wk, wv)]
+        K.qkv_proj(0, hidden.to(DEV), nw.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), *outs, workspace=ws)
+        torch.cuda.synchronize()
+        for name, out, ref in zip("qkv", outs, refs):
+            out = out.cpu()
+            # two roundings apart (summation order, near a power of two the
+            # larger binade's step), plus a normed element one bf16 ulp away
+            # (hardware rsqrt): over 4096 rows some row's largest element
+            # (|x| ~ 5, ulp 2^-5) flips, moving its outputs by up to
+            # 2^-5 * |w| (|w| < 0.12 here), below 2^-8
+            big = torch.maximum(out.float().abs(), ref.float().abs())
+            assert_ulps(out, ref, 2 * ulp(big) + 2.0 ** -8, f"qkv tail split {name}")
+            assert (out.float() == ref).float().mean().item() > 0.9, name
 
 
 def test_decode_layer_chain():
