@@ -80,19 +80,24 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
         skinny_lds_body<bf16_t, false, false, true, HT, false, true>(P.qkv, RopeEpi{}, cb, 0, lds.s);
         __syncthreads();
     }
-    // 2. attention step (every workgroup plans the same ragged split; item w).
-    // The workgroup arrives at barrier 0 first, then plans its item and
-    // fetches its first K/V block (the cache does not depend on phase 1), and
-    // only then waits; a workgroup without an item waits here.
+    // 2. attention step (every workgroup plans the same ragged split).  The
+    // work items go first to the workgroups that ran one phase-1 task (the
+    // first ncb_qkv - nwg ran two), so the items start with their plan and
+    // first K/V block (the cache does not depend on phase 1) while phase 1
+    // finishes.  The workgroup arrives at barrier 0 first, then plans its item
+    // and fetches its first block, and only then waits; a workgroup without
+    // an item does not wait (only the readers of phase 1's output do, and
+    // fewer pollers make the counter's line answer sooner).
+    const int shift = min(max(ncb_qkv - static_cast<int>(nwg), 0), static_cast<int>(nwg));
+    const int item = (w - shift + static_cast<int>(nwg)) % static_cast<int>(nwg);
     grid_arrive(&P.bar[0]);
-    bool passed = false;
-    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, w, 0, 0, lds.d, [&]() {
-        grid_wait(&P.bar[0], nwg);
-        passed = true;
-    });
-    if (!passed) grid_wait(&P.bar[0], nwg);
-    grid_barrier(&P.bar[1], nwg);
-    if (w == 0 && threadIdx.x == 0) P.bar[0] = 0u;  // every workgroup is past barrier 0
+    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, item, 0, 0, lds.d, [&]() { grid_wait(&P.bar[0], nwg); });
+    // Barrier 1: every workgroup arrives; those with an output-projection
+    // task wait for all of them.
+    grid_arrive(&P.bar[1]);
+    if (w < ncb_op) grid_wait(&P.bar[1], nwg);
+    // every workgroup has arrived at barrier 1, so every reader of barrier 0 is past it
+    if (w == 0 && threadIdx.x == 0) P.bar[0] = 0u;
     // 3. output projection + residual
     for (int cb = w; cb < ncb_op; cb += nwg) {
         skinny_lds_body<HT, true, false, false, bf16_t, true, false>(P.op, RopeEpi{}, cb, 0, lds.s);
