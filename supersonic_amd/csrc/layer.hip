@@ -34,7 +34,12 @@ struct LayerParams {
     SkinnyLdsParams qkv;  // phase 1: three segments, NORM staging from the hidden rows
     DecodeParams dec;     // phase 2: fused decode step, ragged plan over the grid
     SkinnyLdsParams op;   // phase 3: attn -> hidden (residual in place)
-    unsigned* bar;        // [3] barrier counters, zero between calls
+    unsigned* bar;        // barrier counters [0..2] and flags [32], [48] (another cache line), zero between calls
+    // > 0: the decode step is expected to have this many work items (one
+    // sequence of length max_kv_len); the last `hint` workgroups then take
+    // them and skip phase 1, which the others share.
+    int hint;
+    int layer_len;        // host: the expected sequence length (max_kv_len), for the hint
 };
 
 constexpr int kLayerThreads = 64 * kSkinnyWaves;  // = 64 * decode_waves(4)
@@ -43,26 +48,29 @@ constexpr int kLayerSpin = 1 << 20;               // bounded barrier wait
 // Every value one phase hands to the next is written and read with
 // device-coherent (sc1) accesses, so the barrier needs no cache writeback or
 // invalidate: each wave waits for its own stores to complete, then one lane
-// arrives and waits for the others.
+// counts the workgroup in; the last to arrive raises a flag on another cache
+// line, which the waiting workgroups poll (polls on the counter's own line
+// measured to hold back the arrivals' atomics).  The arriving lane is the
+// last wave's first: it waits for the count to come back, and wave 0 goes on.
 // Split form: arrive (after this workgroup's stores are complete), do
 // independent work, then wait.
-__device__ __forceinline__ void grid_arrive(unsigned* ctr) {
+constexpr int kArriveThread = kLayerThreads - 64;
+__device__ __forceinline__ void grid_arrive(unsigned* ctr, unsigned* flag, unsigned n) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == kArriveThread) {
+        const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == n - 1) __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
-__device__ __forceinline__ void grid_wait(unsigned* ctr, unsigned n) {
+__device__ __forceinline__ void grid_wait(unsigned* flag) {
     if (threadIdx.x == 0) {
         for (int it = 0; it < kLayerSpin; ++it) {
-            if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= n) break;
+            if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
             __builtin_amdgcn_s_sleep(1);
         }
     }
     __syncthreads();
-}
-__device__ __forceinline__ void grid_barrier(unsigned* ctr, unsigned n) {
-    grid_arrive(ctr);
-    grid_wait(ctr, n);
 }
 
 template <typename HT, bool FP8, int D>
@@ -75,9 +83,19 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
     const int w = blockIdx.x;
     const unsigned nwg = gridDim.x;
     const int ncb_qkv = P.qkv.cb_end[2], ncb_op = P.op.cb_end[2];
-    // 1. input norm + Q/K/V projections
-    for (int cb = w; cb < ncb_qkv; cb += nwg) {
-        skinny_lds_body<bf16_t, false, false, true, HT, false, true>(P.qkv, RopeEpi{}, cb, 0, lds.s);
+    // 1. input norm + Q/K/V projections on the first nq workgroups: column
+    // blocks w, w + nq, ...; a workgroup with two left takes them together
+    // (one staging of the rows, both weight streams in flight)
+    const int nq = static_cast<int>(nwg) - P.hint;
+    for (int cb = w; cb < ncb_qkv && w < nq;) {
+        if (cb + nq < ncb_qkv) {
+            skinny_lds_body<bf16_t, false, false, true, HT, false, true, SkinnyLds, true>(P.qkv, RopeEpi{}, cb, 0,
+                                                                                           lds.s, cb + nq);
+            cb += 2 * nq;
+        } else {
+            skinny_lds_body<bf16_t, false, false, true, HT, false, true>(P.qkv, RopeEpi{}, cb, 0, lds.s);
+            cb += nq;
+        }
         __syncthreads();
     }
     // 2. attention step (every workgroup plans the same ragged split).  The
@@ -88,16 +106,22 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
     // and fetches its first block, and only then waits; a workgroup without
     // an item does not wait (only the readers of phase 1's output do, and
     // fewer pollers make the counter's line answer sooner).
+    // With a hint the expected items sit on the workgroups without phase-1
+    // work (any further item on the others).
     const int shift = min(max(ncb_qkv - static_cast<int>(nwg), 0), static_cast<int>(nwg));
-    const int item = (w - shift + static_cast<int>(nwg)) % static_cast<int>(nwg);
-    grid_arrive(&P.bar[0]);
-    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, item, 0, 0, lds.d, [&]() { grid_wait(&P.bar[0], nwg); });
+    const int item = P.hint > 0 ? (w >= nq ? w - nq : P.hint + w)
+                                : (w - shift + static_cast<int>(nwg)) % static_cast<int>(nwg);
+    grid_arrive(&P.bar[0], &P.bar[32], nwg);
+    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, item, 0, 0, lds.d, [&]() { grid_wait(&P.bar[32]); });
     // Barrier 1: every workgroup arrives; those with an output-projection
     // task wait for all of them.
-    grid_arrive(&P.bar[1]);
-    if (w < ncb_op) grid_wait(&P.bar[1], nwg);
+    grid_arrive(&P.bar[1], &P.bar[48], nwg);
+    if (w < ncb_op) grid_wait(&P.bar[48]);
     // every workgroup has arrived at barrier 1, so every reader of barrier 0 is past it
-    if (w == 0 && threadIdx.x == 0) P.bar[0] = 0u;
+    if (w == 0 && threadIdx.x == 0) {
+        P.bar[0] = 0u;
+        P.bar[32] = 0u;
+    }
     // 3. output projection + residual
     for (int cb = w; cb < ncb_op; cb += nwg) {
         skinny_lds_body<HT, true, false, false, bf16_t, true, false>(P.op, RopeEpi{}, cb, 0, lds.s);
@@ -108,6 +132,7 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
         const unsigned prev = __hip_atomic_fetch_add(&P.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (prev == nwg - 1) {
             P.bar[1] = 0u;
+            P.bar[48] = 0u;
             P.bar[2] = 0u;
         }
     }
@@ -163,6 +188,21 @@ static int launch_layer(int device, hipStream_t st, LayerParams& P) {
     const int grid = std::min(layer_grid<HT, FP8, D>(device), kLayerMaxGrid);
     if (grid <= 0) return SUPERSONIC_ERR_LAUNCH;
     P.dec.target = grid;
+    P.hint = 0;
+    if (P.dec.B == 1 && P.layer_len > 0) {
+        // the device plan for one sequence of the expected length
+        const int64_t l = P.layer_len, Hkv = P.dec.Hkv;
+        int64_t c = (l * Hkv + grid - 1) / grid;
+        c = std::max((c + 15) / 16 * 16, static_cast<int64_t>(P.dec.min_chunk));
+        for (int pass = 0; pass < 4; ++pass) {
+            const int64_t items = std::max<int64_t>(1, (l + c - 1) / c) * Hkv;
+            if (items <= grid) break;
+            c = (c * items + grid - 1) / grid;
+            c = (c + 15) / 16 * 16;
+        }
+        const int64_t items = std::max<int64_t>(1, (l + c - 1) / c) * Hkv;
+        if (2 * items <= grid) P.hint = static_cast<int>(items);
+    }
     hipLaunchKernelGGL((decode_layer_kernel<HT, FP8, D>), dim3(grid), dim3(kLayerThreads), 0, st, P);
     return hipGetLastError() == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
 }
@@ -222,6 +262,7 @@ extern "C" int supersonic_attn_gfx950_decode_layer(
     uint16_t* v_new = reinterpret_cast<uint16_t*>(ws + L.v_new);
     uint16_t* attn = reinterpret_cast<uint16_t*>(ws + L.attn);
     P.bar = reinterpret_cast<unsigned*>(ws + L.bar);
+    P.layer_len = static_cast<int>(max_kv_len);
     // phase 1
     SkinnyLdsParams& q = P.qkv;
     q.xn = hidden;

@@ -125,11 +125,14 @@ struct SkinnyLds : SkinnyLdsBase {
 // NORM: the rows are normalised while staged (XT: element type of p.xn).
 // COH_IN / COH_OUT: the activation rows are read / the outputs written with
 // device-coherent accesses (data exchanged with other workgroups of the same
-// kernel).
+// kernel).  PAIR (plain store epilogue only): a second column block cb2 (or
+// none when cb2 < 0) shares the staged rows, and both blocks' weight loads are
+// in flight together, so two blocks cost little more than one.
 template <typename OT, bool RES, bool ROPE, bool NORM = false, typename XT = bf16_t, bool COH_IN = false,
-          bool COH_OUT = false, typename LdsT = SkinnyLds>
+          bool COH_OUT = false, typename LdsT = SkinnyLds, bool PAIR = false>
 __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const RopeEpi& e, int cb, int b,
-                                                LdsT& L) {
+                                                LdsT& L, int cb2 = -1) {
+    static_assert(!PAIR || (!RES && !ROPE), "pairs take the plain store epilogue");
     uint16_t (&xs)[kXsMax + 16 * 8] = L.xs;
     float (&red)[kSkinnyWaves][256] = L.red;
     // opaque: when several bodies are inlined into one kernel, lane-derived
@@ -192,6 +195,19 @@ __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const 
     u32x4_v wv[kSkinnySteps];
 #pragma unroll
     for (int j = 0; j < kSkinnySteps; ++j) wv[j] = wload(s0 + j);
+    // PAIR: the second block's column segment, weight row and first batch
+    const bool two = PAIR && cb2 >= 0;
+    const int cb2c = two ? cb2 : cb;
+    const int seg2 = cb2c < p.cb_end[0] ? 0 : (cb2c < p.cb_end[1] ? 1 : 2);
+    const int cbs2 = cb2c - (seg2 == 0 ? 0 : (seg2 == 1 ? p.cb_end[0] : p.cb_end[1]));
+    const int n2 = pick3(p.n_seg, seg2);
+    const uint16_t* wrow20 = pick3(p.w, seg2) + b * p.w_bs + static_cast<int64_t>(min(cbs2 * 16 + col, n2 - 1)) * k;
+    auto wload2 = [&](int s) { return ld16(wrow20 + min(s * 32 + kq, k - 8)); };
+    u32x4_v wv2[PAIR ? kSkinnySteps : 1];
+    if constexpr (PAIR) {
+#pragma unroll
+        for (int j = 0; j < kSkinnySteps; ++j) wv2[j] = wload2(s0 + j);
+    }
     // RES: the residual element this thread adds in the epilogue, loaded now so
     // that its round trip overlaps the weight stream (clamped, branch-free)
     float res_v = 0.f;
@@ -252,11 +268,15 @@ __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const 
     // 4. the weight stream, A operand from LDS
     const bool mvalid = col < m;
     const uint16_t* xrow = xs + col * ldx + kq;
-    f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4_v acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
     for (int sb = s0; sb < s1; sb += kSkinnySteps) {
         if (sb > s0) {
 #pragma unroll
             for (int j = 0; j < kSkinnySteps; ++j) wv[j] = wload(sb + j);
+            if constexpr (PAIR) {
+#pragma unroll
+                for (int j = 0; j < kSkinnySteps; ++j) wv2[j] = wload2(sb + j);
+            }
         }
 #pragma unroll
         for (int j = 0; j < kSkinnySteps; ++j) {
@@ -264,6 +284,7 @@ __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const 
             const u32x4_v a = (s < s1 && mvalid && s * 32 + kq < k)
                                   ? *reinterpret_cast<const u32x4_v*>(xrow + s * 32) : zero;
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(wv[j]), acc, 0, 0, 0);
+            if constexpr (PAIR) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(wv2[j]), acc2, 0, 0, 0);
         }
     }
 #pragma unroll
@@ -281,6 +302,26 @@ __device__ __forceinline__ void skinny_lds_body(const SkinnyLdsParams& p, const 
                 if constexpr (RES) y = bf16_round(res_v + y);
                 if constexpr (COH_OUT) store_f32_agent<OT>(static_cast<OT*>(pick3(p.out, seg)), o, y);
                 else store_f32<OT>(static_cast<OT*>(pick3(p.out, seg)), o, y);
+            }
+        }
+        if constexpr (PAIR) {
+            if (two) {
+                __syncthreads();  // every thread has read red for the first block
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave][(4 * (lane >> 4) + i) * 16 + col] = acc2[i];
+                __syncthreads();
+                if (tid < 256) {
+                    const int row = tid >> 4, c = cbs2 * 16 + (tid & 15);
+                    if (row < m && c < n2) {
+                        float sum = 0.f;
+#pragma unroll
+                        for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][tid];
+                        const float y = bf16_round(sum);
+                        const int64_t o = b * p.o_bs + static_cast<int64_t>(row) * n2 + c;
+                        if constexpr (COH_OUT) store_f32_agent<OT>(static_cast<OT*>(pick3(p.out, seg2)), o, y);
+                        else store_f32<OT>(static_cast<OT*>(pick3(p.out, seg2)), o, y);
+                    }
+                }
             }
         }
     } else {
