@@ -104,15 +104,32 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
     // first K/V block (the cache does not depend on phase 1) while phase 1
     // finishes.  The workgroup arrives at barrier 0 first, then plans its item
     // and fetches its first block, and only then waits; a workgroup without
-    // an item does not wait (only the readers of phase 1's output do, and
-    // fewer pollers make the counter's line answer sooner).
+    // an item does not wait (only the readers of phase 1's output do).
     // With a hint the expected items sit on the workgroups without phase-1
     // work (any further item on the others).
     const int shift = min(max(ncb_qkv - static_cast<int>(nwg), 0), static_cast<int>(nwg));
     const int item = P.hint > 0 ? (w >= nq ? w - nq : P.hint + w)
                                 : (w - shift + static_cast<int>(nwg)) % static_cast<int>(nwg);
     grid_arrive(&P.bar[0], &P.bar[32], nwg);
-    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, item, 0, 0, lds.d, [&]() { grid_wait(&P.bar[32]); });
+    bool had_item = false;
+    decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, item, 0, 0, lds.d, [&]() {
+        grid_wait(&P.bar[32]);
+        had_item = true;
+    });
+    if (!had_item && w < ncb_op) {
+        // An output-projection workgroup without a decode item copies its
+        // first task's weight rows into an LDS sink while the items run, so
+        // that phase 3 finds them in this XCD's L2.  (The copies complete
+        // before it arrives at barrier 1, which waits for its loads.)
+        const int k = P.op.k;
+        const int bytes = min(kSkinnyCols, P.op.n_seg[0] - w * kSkinnyCols) * k * 2;
+        const __amdgpu_buffer_rsrc_t r =
+            uniform_rsrc(reinterpret_cast<const uint8_t*>(P.op.w[0] + static_cast<int64_t>(w) * kSkinnyCols * k), bytes);
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        for (int off = wave * 1024; off < bytes; off += kSkinnyWaves * 1024)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds.s.xs, 16,
+                                                     off + lane * 16, 0, 0, 0);
+    }
     // Barrier 1: every workgroup arrives; those with an output-projection
     // task wait for all of them.
     grid_arrive(&P.bar[1], &P.bar[48], nwg);
