@@ -14,9 +14,10 @@
 //   3. the output projection with the residual add, in place on the hidden rows.
 // Every value one phase hands to the next is stored and loaded with
 // device-coherent accesses, so a barrier is: each wave waits for its own
-// stores, one lane bumps a counter and spins (bounded) until all workgroups
-// have arrived.  Launch fill and drain are paid once per layer instead of
-// once per kernel.
+// stores, one lane bumps a counter, the last to arrive raises a flag, and only
+// the workgroups that read the previous phase's output wait (bounded) for the
+// flag.  Launch fill and drain are paid once per layer instead of once per
+// kernel.
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>

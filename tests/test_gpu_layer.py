@@ -19,12 +19,12 @@ from supersonic_amd import kernel_ffi as K
 pytestmark = pytest.mark.gpu
 
 
-def layer_case(seed, B, Hq, Hkv, D, rot, hid, lens, fp8=False, hidden_f32=False, page=None):
+def layer_case(seed, B, Hq, Hkv, D, rot, hid, lens, fp8=False, hidden_f32=False, page=None, max_extra=0):
     g = gen(seed)
     cap = max(lens) + 1
     if page:
         cap = (cap + page - 1) // page * page
-    c = dict(B=B, Hq=Hq, Hkv=Hkv, D=D, rot=rot, hid=hid, lens=lens, fp8=fp8, page=page)
+    c = dict(B=B, Hq=Hq, Hkv=Hkv, D=D, rot=rot, hid=hid, lens=lens, fp8=fp8, page=page, max_extra=max_extra)
     c["hidden"] = O.randn_bf16(g, B, hid)
     c["nw"] = O.randn_bf16(g, hid, std=0.1)
     c["wq"], c["wk"], c["wv"] = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (Hq * 2 * D, Hkv * D, Hkv * D))
@@ -76,7 +76,7 @@ def run_layer(c, ws):
     pos = torch.tensor(c["lens"], dtype=torch.int32, device=DEV)
     K.decode_layer(0, h, dev(c["nw"]), dev(c["wq"]), dev(c["wk"]), dev(c["wv"]), dev(c["qw"]), dev(c["kw"]),
                    dev(c["wo"]), dev(c["cos"]), dev(c["sin"]), pos, cache, ws, q_heads=c["Hq"], kv_heads=c["Hkv"],
-                   head_dim=c["D"], rotary_dim=c["rot"], max_kv_len=max(c["lens"]) + 1)
+                   head_dim=c["D"], rotary_dim=c["rot"], max_kv_len=max(c["lens"]) + 1 + c["max_extra"])
     torch.cuda.synchronize()
     return h.float().cpu(), cache
 
@@ -115,6 +115,10 @@ def check_layer(c, out, cache, ref, v_ref):
 
 CASES = {
     "config1": dict(B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[2048]),
+    # one sequence whose max_kv_len overstates its length: the layer's guess
+    # of the decode work items (and of which workgroups skip phase 1) is wrong
+    "config1_loose_max_kv_len": dict(B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[2048], max_extra=5000),
+    "one_short_sequence": dict(B=1, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[40]),
     "config2_b4_ragged": dict(B=4, Hq=16, Hkv=4, D=256, rot=64, hid=4096, lens=[3000, 17, 1500, 0]),
     "d128": dict(B=2, Hq=8, Hkv=2, D=128, rot=32, hid=2048, lens=[700, 2100]),
     "fp8": dict(B=2, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[1200, 333], fp8=True),
