@@ -16,7 +16,11 @@
 // (buffer range / offset checks), so any m, n and k % 8 == 0 work.
 // Workgroups are mapped to tiles XCD by XCD: consecutive tiles of the order
 // (bands of 8 m-tiles, n-major within a band) go to one XCD, whose L2 then
-// serves the shared rows of a and w.
+// serves the shared rows of a and w.  One workgroup fits a CU (144 KB of LDS),
+// so the tiles run in rounds of one per CU; when the last round would occupy at
+// most half the CUs, its tiles run as two workgroups each, over the two halves
+// of k, the first handing its fp32 accumulators to the second through the
+// caller's workspace.
 #include <algorithm>
 
 #include "common.hpp"
