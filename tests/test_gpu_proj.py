@@ -162,6 +162,8 @@ def test_o_proj_two_roundings(k):
     (33, 300, 520, None), (100, 256, 512, None), (3, 64, 36, None),
     # the streaming kernel with 2..4 row blocks, and its k split over workgroups
     (16, 4096, 4096, 64), (33, 300, 520, 64), (64, 256, 1024, 64), (12, 512, 8192, None), (40, 512, 8192, 64),
+    # the tiled GEMM with the residual epilogue after a tail split (288 tiles)
+    (4096, 4608, 512, None),
 ])
 @pytest.mark.parametrize("hdt", [torch.bfloat16, torch.float32])
 def test_o_proj_residual_matches_oracle(rows, hidden_dim, attn_dim, max_m, hdt, monkeypatch):
