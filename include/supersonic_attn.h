@@ -276,11 +276,14 @@ int supersonic_attn_gfx950_prefill(
  * :5019-5101) and rms_norm_rows_model + matmul_proj of prefill_engine.rs:1951-2117.
  * A norm kernel writes the normed rows once (workspace), then rows <= 12
  * (SUPERSONIC_PROJ_SKINNY_MAX_M) with q/kv_out_dim % 16 == 0 take one
- * weight-streaming launch over the three matrices; otherwise one hipBLASLt GEMM
- * per matrix.  hidden_dim % 8 == 0.  Asynchronous on `stream`.  workspace:
- * caller device memory of at least supersonic_attn_gfx950_qkv_proj_workspace_size()
- * bytes, zero-filled before its first use and not written by the caller
- * between calls (split-k arrival counters that every call leaves at zero);
+ * weight-streaming launch over the three matrices; otherwise one launch of the
+ * hand-written MFMA GEMM over the three matrices as column segments
+ * (SUPERSONIC_PROJ_GEMM=hipblaslt: one hipBLASLt GEMM per matrix instead).
+ * hidden_dim % 8 == 0.  Asynchronous on `stream`.  workspace: caller device
+ * memory of at least supersonic_attn_gfx950_qkv_proj_workspace_size() bytes,
+ * zero-filled before its first use and not written by the caller between calls
+ * (split-k arrival counters and the GEMM's tail-split flags, which every call
+ * leaves at zero);
  * calls sharing it must not overlap.  NULL: library-owned buffers per device
  * (grown on demand; overlapping calls on one device then race). */
 size_t supersonic_attn_gfx950_qkv_proj_workspace_size(
@@ -359,9 +362,11 @@ int supersonic_attn_gfx950_decode_layer(
  * (hidden_dtype 1, the megakernel's hidden_f32).  Replaces the megakernel's
  * step G (full_attention_4b.hip:5481-5577) and matmul_proj + residual_add of
  * prefill_engine.rs:2308-2334.  rows <= 12 (SUPERSONIC_PROJ_SKINNY_MAX_M, at most 64) with attn_dim % 8 == 0: one
- * HBM-streaming MFMA kernel with the residual fused; otherwise hipBLASLt and a
- * residual kernel.  Asynchronous on `stream`.  workspace: split-k partials
- * and arrival counters, or the GEMM output rows; caller device memory of at
+ * HBM-streaming MFMA kernel with the residual fused; otherwise the hand-written
+ * MFMA GEMM with the residual add in its epilogue, in place
+ * (SUPERSONIC_PROJ_GEMM=hipblaslt: hipBLASLt and a residual kernel).
+ * Asynchronous on `stream`.  workspace: split-k partials and arrival counters,
+ * the GEMM's tail-split flags and partials, or (hipBLASLt) the GEMM output rows; caller device memory of at
  * least supersonic_attn_gfx950_o_proj_workspace_size() bytes under the same
  * rules as supersonic_attn_gfx950_qkv_proj's, or NULL for library-owned
  * buffers per device. */
