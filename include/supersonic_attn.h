@@ -141,7 +141,8 @@ int supersonic_qwen35_hip_split_qgate(
  * included, of prefill_engine.rs:356-414).  Replaces
  * kernels/full_attention_bridge_4b.cpp:3683-3704 (kernel full_attention_4b.hip:2513-2575),
  * bound at prefill_ffi.rs:782-792.  m <= 12 (SUPERSONIC_PROJ_SKINNY_MAX_M): HBM-streaming MFMA kernel; larger m:
- * hipBLASLt.  Status: 272 bad dtype, 270 launch, 271 sync. */
+ * the hand-written tiled MFMA GEMM (SUPERSONIC_PROJ_GEMM=hipblaslt: hipBLASLt).
+ * Status: 272 bad dtype, 270 launch, 271 sync. */
 int supersonic_qwen35_4b_hip_matmul_rhs_transposed_tiled(
     int dtype, size_t device_ordinal, size_t batch_elems, int m, int n, int k,
     const void* lhs, const void* rhs, void* out);
