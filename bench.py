@@ -223,12 +223,12 @@ class Workloads:
 
     def decode_cfg1(self):
         """Config 1: Qwen3.5-0.8B-like decode, B=1, 8/2 heads, 2048 cached tokens."""
-        r = self.decode_result("config 1, B=1, Hq 8, Hkv 2, L=2048", 1, [2048], 8, 2, 256, 64)
+        r = self.decode_result("config 1, B=1, Hq 8, Hkv 2, L=2048", 1, [2048], 8, 2, 256, 64, traffic_key="decode_cfg1")
         r["gbs"] = round(r["gbs"], 2)
         return r
 
     def decode1(self):
-        r = self.decode_result("config 2, B=1, L=32768", 1, [32768], 16, 4, 256, 64)
+        r = self.decode_result("config 2, B=1, L=32768", 1, [32768], 16, 4, 256, 64, traffic_key="decode1")
         r["gbs"] = round(r["gbs"], 2)
         return r
 
@@ -237,7 +237,7 @@ class Workloads:
         g = torch.Generator().manual_seed(4)
         lens = torch.randint(1024, 16385, (16,), generator=g).tolist()
         r = self.decode_result("config 4, FP8 e4m3 KV, B=16, L~U[1024,16384]", 16, lens, 16, 4, 256, 64,
-                               fp8=True, cap=16385)
+                               fp8=True, cap=16385, traffic_key="fp8")
         r["lens_sum"] = sum(lens)
         return r
 
@@ -463,7 +463,7 @@ class Workloads:
             res[label + "oproj_tflops"] = o_flops / (o_ms * 1e-3) / 1e12
         ach = o_flops / (res["oproj_ms"] * 1e-3) / 1e12
         res["roofline"] = {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                           "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                           "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": measured_traffic("gemm_oproj"),
                            "kernel": "gemm_bt_kernel (o_proj + residual epilogue)"}
         return res
 
