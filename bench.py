@@ -129,25 +129,31 @@ class Workloads:
         return evs
 
     def timed(self, step, n_copies=1):
-        """Run warmup + steps of `step(i, before, after)`; returns whole-step ms and
-        the dominant kernel's mean ms (events armed around it)."""
+        """Run warmup + steps of `step(i)`; returns whole-step ms and the
+        dominant kernel's mean ms.  The whole-step time comes from `steps` steps
+        with nothing but the workload between two events; the kernel time from
+        another `steps` steps with an event pair armed around the kernel (the
+        event records add about 10 us between kernels, so they stay out of the
+        whole-step timing)."""
         torch, K = self.torch, self.K
         for i in range(self.warmup):
             step(i % n_copies)
         torch.cuda.synchronize()
-        kb = self.events(self.steps)
-        ka = self.events(self.steps)
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
         t0.record()
         for i in range(self.steps):
-            K.set_profile_events(kb[i], ka[i])
             step(i % n_copies)
         t1.record()
         torch.cuda.synchronize()
-        K.set_profile_events(None, None)
         step_ms = t0.elapsed_time(t1) / self.steps
+        kb = self.events(self.steps)
+        ka = self.events(self.steps)
+        for i in range(self.steps):
+            K.set_profile_events(kb[i], ka[i])
+            step(i % n_copies)
+        torch.cuda.synchronize()
+        K.set_profile_events(None, None)
         kern = [kb[i].elapsed_time(ka[i]) for i in range(self.steps)]
         return step_ms, statistics.mean(kern), kern
 
