@@ -119,6 +119,7 @@ CASES = {
     # of the decode work items (and of which workgroups skip phase 1) is wrong
     "config1_loose_max_kv_len": dict(B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[2048], max_extra=5000),
     "one_short_sequence": dict(B=1, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[40]),
+    "one_sequence_fp8_paged": dict(B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[3000], fp8=True, page=64),
     "config2_b4_ragged": dict(B=4, Hq=16, Hkv=4, D=256, rot=64, hid=4096, lens=[3000, 17, 1500, 0]),
     "d128": dict(B=2, Hq=8, Hkv=2, D=128, rot=32, hid=2048, lens=[700, 2100]),
     "fp8": dict(B=2, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[1200, 333], fp8=True),
