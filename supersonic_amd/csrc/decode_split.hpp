@@ -125,7 +125,7 @@ template <int D, int GP>
 struct DecodeLds {
     static constexpr int NW = decode_waves(GP);
     float smem[NW * GP * D];        // q staging, then the wave merge
-    float p_s[NW][16][GP];          // per-wave probabilities
+    float p_s[NW][16][16];          // per-wave probabilities (heads past GP: padding that every lane may write)
     float kn_s[D], vn_s[D];         // the new token (fused owner split)
     float ml_s[NW][GP][2];
     u32x4_v qop_s[(D / 32) * 64];   // Q as the MFMA A operand
@@ -162,7 +162,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     constexpr int NW = decode_waves(GP);
     constexpr int NT = 64 * NW;
     float (&smem)[NW * GP * D] = L.smem;
-    float (&p_s)[NW][16][GP] = L.p_s;
+    float (&p_s)[NW][16][16] = L.p_s;
     float (&kn_s)[D] = L.kn_s;
     float (&vn_s)[D] = L.vn_s;
     float (&ml_s)[NW][GP][2] = L.ml_s;
@@ -564,7 +564,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             m[i] = mn;
             pr[i] = pe * vsc;
         }
-        if (4 * (lane >> 4) < GP) {
+        {  // every lane: those of heads past GP write the padding (with an
+           // exec-masked store here the layer kernel reloaded a spilled
+           // register inside its main loop, a wait for every load in flight)
             f32x4_v pv = {pr[0], pr[1], pr[2], pr[3]};
             *reinterpret_cast<f32x4_v*>(&p_s[wave][n_s][4 * (lane >> 4)]) = pv;
         }
