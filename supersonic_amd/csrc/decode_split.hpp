@@ -24,6 +24,11 @@ struct DecodeParams {
     // workgroup gets about the same number of tokens whatever the lengths;
     // chunk and nsplit are then unused.
     int ragged, B, target, min_chunk;
+    // 1: the grid has exactly `target` workgroups (the persistent layer), so
+    // the plan must not exceed target items: if the chunk growth below has
+    // not got there, every sequence takes one split (B * Hkv <= target is
+    // checked on the host).  0: the grid holds target + B * Hkv workgroups.
+    int strict;
     int det;                  // 1: static block order (bit-reproducible), 0: blocks claimed from an LDS counter
     float scale_log2;         // softmax scale * log2(e)
     int fused;
@@ -197,7 +202,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             // until the items fit (a few passes; uniform lengths need none).
             int64_t c = (tot * p.Hkv + p.target - 1) / p.target;
             c = max((c + 15) / 16 * 16, static_cast<int64_t>(p.min_chunk));
-            for (int pass = 0; pass < 4; ++pass) {
+            bool fits = false;
+            for (int pass = 0; pass < 5; ++pass) {
                 int64_t items = 0;
                 for (int b0 = 0; b0 < p.B; b0 += 64) {
                     const int bi = b0 + lane;
@@ -207,9 +213,18 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
 #pragma unroll
                 for (int o = 1; o < 64; o <<= 1) items += __shfl_xor(items, o);
                 items *= p.Hkv;
-                if (items <= p.target) break;
+                fits = items <= p.target;
+                if (fits || pass == 4) break;
                 c = (c * items + p.target - 1) / p.target;
                 c = (c + 15) / 16 * 16;
+            }
+            if (p.strict && !fits) {
+                // four growth steps did not get there: one split per sequence
+                int64_t mx = 0;
+                for (int b0 = 0; b0 < p.B; b0 += 64) mx = max(mx, static_cast<int64_t>(len_of(b0 + lane)));
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) mx = max(mx, __shfl_xor(mx, o));
+                c = max(c, (mx + 15) / 16 * 16);
             }
             const int ch = static_cast<int>(c);
             if (lane == 0) plan_s[0] = -1;

@@ -205,7 +205,10 @@ template <typename HT, bool FP8, int D>
 static int launch_layer(int device, hipStream_t st, LayerParams& P) {
     const int grid = std::min(layer_grid<HT, FP8, D>(device), kLayerMaxGrid);
     if (grid <= 0) return SUPERSONIC_ERR_LAUNCH;
+    // one workgroup per item: every (sequence, kv head) needs one
+    if (P.dec.B * P.dec.Hkv > grid) return SUPERSONIC_ERR_RANGE;
     P.dec.target = grid;
+    P.dec.strict = 1;
     P.hint = 0;
     if (P.dec.B == 1 && P.layer_len > 0) {
         // the device plan for one sequence of the expected length

@@ -126,6 +126,12 @@ CASES = {
     "f32_hidden": dict(B=3, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[64, 65, 900], hidden_f32=True),
     "paged": dict(B=3, Hq=16, Hkv=4, D=256, rot=64, hid=2048, lens=[700, 64, 1500], page=64),
     "paged_fp8": dict(B=2, Hq=8, Hkv=2, D=128, rot=32, hid=1024, lens=[1000, 129], fp8=True, page=64),
+    # 16 x 16 (sequence, kv head) pairs on a 256-workgroup grid, lengths for
+    # which four chunk-growth steps of the plan still leave 272 items: the
+    # layer must fall back to one split per sequence, not drop 16 items
+    "many_kv_heads_ragged": dict(B=16, Hq=16, Hkv=16, D=128, rot=32, hid=2048,
+                                 lens=[1105, 672, 613, 2390, 1186, 1479, 1618, 2247, 532, 1202, 471, 1959, 2993, 982,
+                                       198, 1262]),
 }
 
 
