@@ -412,6 +412,12 @@ class Workloads:
                 "prefill_frac": fl / (p_kern * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 "decode_gbs": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9,
                 "decode_frac": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                # the step's combined bound max(bytes / HBM peak, flops / MFMA peak)
+                # against the measured step (the two calls run one after the other)
+                "combined_bound_ms": max((kv_bytes + 32 * Hq * D * 2) / (HBM_PEAK_GBS * 1e9),
+                                         fl / (BF16_PEAK_TFLOPS * 1e12)) * 1e3,
+                "combined_frac": max((kv_bytes + 32 * Hq * D * 2) / (HBM_PEAK_GBS * 1e9),
+                                     fl / (BF16_PEAK_TFLOPS * 1e12)) * 1e3 / tot_ms,
                 "lens_sum": sum(lens)}
 
     def oproj(self):
