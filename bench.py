@@ -383,7 +383,8 @@ class Workloads:
                 "tflops_step": fl / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms, "kernel_ms": kern_ms,
                 "stage_ms": step_ms - kern_ms, "flops": fl,
                 "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                             "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+                             "traffic": measured_traffic("prefill_fp8"),
                              "kernel": "prefill_kernel (bf16 MFMA over the dequantised prefix)"}}
 
     def mixed(self):
@@ -548,7 +549,7 @@ class Workloads:
         return {"workload": "input norm + Q/K/V projections + QK norm + RoPE + KV append, 8 rows, 4096 -> 16/4 heads",
                 "ms_per_step": step_ms, "kernel_ms": kern_ms, "bytes": kern_bytes,
                 "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic("qkv_rope"),
                              "kernel": "input_norm_kernel + skinny_lds_kernel (fused norm/RoPE epilogue), events around both",
                              "bytes_per_launch": kern_bytes}}
 
