@@ -615,8 +615,15 @@ class Workloads:
                 K.decode_layer(0, hidden, nw, wq, wk, wv, qw, kw, wo, cos, sin, pos, cache, lws, q_heads=Hq,
                                kv_heads=Hkv, head_dim=D, rotary_dim=rot, max_kv_len=L + 1, stream=st)
             pers_ms = timed_on_stream(persistent)
+            # the same kernel through an ordinary launch (no co-residency guarantee)
+            os.environ["SUPERSONIC_LAYER_LAUNCH"] = "plain"
+            try:
+                plain_ms = timed_on_stream(persistent)
+            finally:
+                del os.environ["SUPERSONIC_LAYER_LAUNCH"]
             res[name] = {"eager_us_per_layer": round(eager_ms * 1e3, 2), "graph_us_per_layer": round(graph_ms * 1e3, 2),
-                         "persistent_us_per_layer": round(pers_ms * 1e3, 2), "launches_per_layer": 4}
+                         "persistent_us_per_layer": round(pers_ms * 1e3, 2),
+                         "persistent_plain_launch_us_per_layer": round(plain_ms * 1e3, 2), "launches_per_layer": 4}
             del kc, vc, cache, graph
             torch.cuda.empty_cache()
         return {"workload": "decode layer (input norm + Q/K/V projections, fused decode, o_proj + residual): eager "

@@ -44,6 +44,13 @@ extern "C" {
 #define SUPERSONIC_ERR_SYNC 1008
 #define SUPERSONIC_ERR_RANGE 1009
 #define SUPERSONIC_ERR_CACHE 1010
+/* The device cannot co-schedule the persistent layer's grid (no cooperative
+ * launch, or the grid does not fit at once). */
+#define SUPERSONIC_ERR_COOPERATIVE 1011
+/* Bits of supersonic_attn_gfx950_wait_status(): a bounded wait gave up. */
+#define SUPERSONIC_WAIT_LAYER_BARRIER 1u /* persistent layer: grid barrier */
+#define SUPERSONIC_WAIT_DECODE_MERGE 2u  /* split-K merge: a partial never arrived */
+#define SUPERSONIC_WAIT_GEMM_TAIL 4u     /* prefill GEMM: a tail tile's first k half never arrived */
 
 /* ------------------------------------------------------------------------- */
 /* 1. Drop-in reference symbols                                              */
@@ -283,8 +290,8 @@ int supersonic_attn_gfx950_prefill(
  * hidden_dim % 8 == 0.  Asynchronous on `stream`.  workspace: caller device
  * memory of at least supersonic_attn_gfx950_qkv_proj_workspace_size() bytes,
  * zero-filled before its first use and not written by the caller between calls
- * (split-k arrival counters and the GEMM's tail-split flags, which every call
- * leaves at zero);
+ * (split-k arrival counters, which every call leaves at zero, and the GEMM's
+ * tail hand-over counts, which every call leaves pairwise equal);
  * calls sharing it must not overlap.  NULL: library-owned buffers per device
  * (grown on demand; overlapping calls on one device then race). */
 size_t supersonic_attn_gfx950_qkv_proj_workspace_size(
@@ -336,8 +343,9 @@ int supersonic_attn_gfx950_qkv_proj_rope(
  * hidden [batch, hidden_dim] bf16 (hidden_dtype 2) or f32 holding bf16 values
  * (1); weights as supersonic_attn_gfx950_qkv_proj / _o_proj_residual; cache,
  * positions, tables as supersonic_attn_gfx950_decode.  One workgroup per
- * compute unit, three phases separated by device-wide barriers (every
- * workgroup of the grid is resident at once).  Limits: batch <= 16,
+ * compute unit, three phases separated by device-wide barriers, launched
+ * cooperatively so that every workgroup of the grid is resident at once
+ * (SUPERSONIC_ERR_COOPERATIVE when the device cannot do that).  Limits: batch <= 16,
  * batch * hidden_dim <= 32768 and batch * q_heads * head_dim <= 32768,
  * hidden_dim % 16 == 0, head_dim 128/256, q_heads / kv_heads <= 4, 16-byte
  * aligned hidden and weights (otherwise SUPERSONIC_ERR_RANGE: use the
@@ -401,6 +409,20 @@ void supersonic_attn_gfx950_set_profile_events(void* before, void* after);
  * SUPERSONIC_ERR_NULL. */
 int supersonic_attn_rope_tables(size_t rotary_dim, size_t max_pos, double theta, uint16_t* cos_out,
                                 uint16_t* sin_out);
+
+/* Bounded waits (no reference counterpart).  Waits that depend on another
+ * workgroup (the persistent layer's grid barriers, the split-K merge's poll
+ * for partials in flight, the prefill GEMM's tail hand-over) give up after a bounded number of polls, set a bit
+ * in a sticky per-device error word and let the kernel exit normally.  This
+ * call synchronises `stream`, returns the OR of the SUPERSONIC_WAIT_* bits
+ * set since the last call in *bits and clears them.  A set bit means some
+ * output since then is wrong, and the workspace of the call that set it must be
+ * zero-filled again before reuse.  Under the documented preconditions
+ * (cooperative launch, zero-filled workspaces) no wait gives up.  The
+ * synchronous drop-ins check the word themselves and return their sync-failure
+ * status.  SUPERSONIC_WAIT_POLLS (environment) overrides the poll bound, for
+ * tests that force the give-up path. */
+int supersonic_attn_gfx950_wait_status(size_t device_ordinal, void* stream, uint32_t* bits);
 
 /* Library version string. */
 const char* supersonic_attn_version(void);

@@ -6,6 +6,7 @@
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <cstdlib>
 
 namespace ssa {
 
@@ -179,6 +180,17 @@ __device__ __forceinline__ float part_dec(uint32_t w) { return __uint_as_float(~
 __device__ __forceinline__ void store_part(float* p, float v) { store_agent_u32(reinterpret_cast<uint32_t*>(p), part_enc(v)); }
 constexpr int kMergePoll = 1 << 16;
 
+// Sticky error word of this code object (each translation unit holds its own
+// copy on every GPU): a bounded wait that gives up sets its bit and the kernel
+// carries on to a normal exit.  The host reads and clears it with
+// take_wait_error(); supersonic_attn_gfx950_wait_status() reports the OR of
+// every translation unit's word.
+enum : unsigned { kWaitLayerBarrier = 1u, kWaitDecodeMerge = 2u, kWaitGemmTail = 4u };
+static __device__ unsigned g_wait_error;
+__device__ __forceinline__ void wait_expired(unsigned bit) {
+    __hip_atomic_fetch_or(&g_wait_error, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Device-coherent (sc1) vector accesses of 4 << L2B bytes per lane through a
 // buffer resource on a wave-uniform base: one instruction for a lane's
 // 4-16 bytes (coherent accesses cost about as much per instruction as per
@@ -288,6 +300,33 @@ struct ProfileEvents {
     hipEvent_t after = nullptr;
 };
 ProfileEvents take_profile_events();
+
+// Poll budget of a bounded wait: SUPERSONIC_WAIT_POLLS when set (read per
+// call; a small value lets a test force the give-up path), else `dflt`.
+inline int wait_polls(int dflt) {
+    const char* v = getenv("SUPERSONIC_WAIT_POLLS");
+    if (!v || !*v) return dflt;
+    const long n = strtol(v, nullptr, 10);
+    return n < 0 ? 0 : (n > (1L << 30) ? (1 << 30) : static_cast<int>(n));
+}
+
+// Reads and clears this translation unit's error word on the current device
+// (synchronous; the caller has synchronised the work it asks about).
+static inline hipError_t take_wait_error(unsigned* bits) {
+    unsigned v = 0;
+    hipError_t e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_wait_error), sizeof(v), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return e;
+    if (v) {
+        const unsigned zero = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_error), &zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+    }
+    *bits |= v;
+    return e;
+}
+// Per translation unit readers (decode.hip, layer.hip, gemm.hip).
+hipError_t take_wait_error_decode(unsigned* bits);
+hipError_t take_wait_error_layer(unsigned* bits);
+hipError_t take_wait_error_gemm(unsigned* bits);
 
 inline unsigned grid1d(size_t n, int block) {
     return static_cast<unsigned>((n + block - 1) / block);

@@ -188,6 +188,7 @@ static int run_decode(DecodeRequest& r) {
     p.det = decode_deterministic();
     p.scale_log2 = r.scale * kLog2e;
     p.arrivals = static_cast<unsigned*>(ws);
+    p.merge_polls = wait_polls(kMergePoll);
     p.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes);
     p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes + align256(rows * r.D * sizeof(float)));
     p.gate = r.gate;
@@ -280,8 +281,14 @@ static int decode_flat_common(int dtype, size_t device, size_t B, size_t Hq, siz
     if (rc == SUPERSONIC_ERR_LAUNCH || rc == SUPERSONIC_ERR_WORKSPACE) return 402;
     if (rc != 0) return 401;
     if (hipDeviceSynchronize() != hipSuccess) return 403;
+    // a merge that gave up on a partial (workspace not in its between-calls
+    // state) wrote a wrong row: report it as the sync failure
+    unsigned werr = 0;
+    if (take_wait_error(&werr) != hipSuccess || werr != 0) return 403;
     return 0;
 }
+
+hipError_t take_wait_error_decode(unsigned* bits) { return take_wait_error(bits); }
 
 }  // namespace ssa
 
@@ -380,29 +387,24 @@ extern "C" int supersonic_attn_gfx950_decode(
 constexpr size_t kScratchBytes = 8u << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
-__global__ void zero_u32_kernel(unsigned* p, int n) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
-}
-
 namespace {
 std::mutex g_scratch_mu;
 std::vector<void*> g_scratch_ptr;  // device address of `scratch`, per device
 }  // namespace
 
 // Device address of this device's `scratch` (the current device must be
-// `device`), looked up once per device.  The first lookup on a device also
-// clears the array (arrival counters and partial slots) with a kernel on `st`
-// (every later call leaves them at zero).  NULL if the lookup fails.
-static void* scratch_for(int device, hipStream_t st) {
+// `device`), looked up once per device.  The array is zero when the code
+// object is loaded (static device storage), which is the state the kernels
+// need (arrival counters and partial slots at zero) and every call leaves it
+// in, so no clearing work is enqueued: a first call under stream capture
+// records nothing extra.  NULL if the lookup fails.
+static void* scratch_for(int device) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (device < 0) return nullptr;
     if (static_cast<size_t>(device) >= g_scratch_ptr.size()) g_scratch_ptr.resize(device + 1, nullptr);
     if (!g_scratch_ptr[device]) {
         void* ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
-        hipLaunchKernelGGL(zero_u32_kernel, dim3(256), dim3(256), 0, st, static_cast<unsigned*>(ptr),
-                           static_cast<int>(kScratchBytes / sizeof(unsigned)));
-        if (hipGetLastError() != hipSuccess) return nullptr;
         g_scratch_ptr[device] = ptr;
     }
     return g_scratch_ptr[device];
@@ -424,7 +426,7 @@ extern "C" int supersonic_attn_gfx950_decode_noalloc(
     void* ws;
     {
         ScopedDevice scoped(static_cast<int>(device_ordinal));
-        ws = scratch_for(static_cast<int>(device_ordinal), static_cast<hipStream_t>(stream));
+        ws = scratch_for(static_cast<int>(device_ordinal));
     }
     if (!ws) return SUPERSONIC_ERR_WORKSPACE;
     return supersonic_attn_gfx950_decode(device_ordinal, stream, kv_dtype, batch, q_heads, kv_heads, head_dim,

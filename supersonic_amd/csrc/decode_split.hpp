@@ -43,6 +43,7 @@ struct DecodeParams {
     float* part_o;            // [rows, D], row of (b, h, split) = pre_b * Hq + h * n_b + split
     float* part_ml;           // [rows, 2] (max in log2 units, sum)
     unsigned* arrivals;       // [B, Hkv] split arrival counters, zero between calls
+    int merge_polls;          // bound of the merge's poll for partials in flight (kMergePoll)
     const uint16_t* gate;     // NULL, or gate element (b, h, d) at b*g_bstride + h*g_hstride + d
     int64_t g_bstride, g_hstride;
     void* out;                // [B, Hq*D] of QT
@@ -863,7 +864,11 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 // every split has arrived, so its partial is stored or on its
                 // way (the cap only guards against a workspace that was not
                 // zero-filled)
-                if (!__builtin_amdgcn_ballot_w64(miss) || it >= kMergePoll) break;
+                if (!__builtin_amdgcn_ballot_w64(miss)) break;
+                if (it >= p.merge_polls) {
+                    if (lane == 0) wait_expired(kWaitDecodeMerge);
+                    break;
+                }
                 __builtin_amdgcn_s_sleep(2);
             }
             const bool own_lane = lane < MCH && s0 + lane == split && split < sp_hi;  // inside this wave's range

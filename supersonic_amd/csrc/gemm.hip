@@ -55,10 +55,11 @@ struct GemmKParams {
     // Tail split: the first `full` tiles of the order run whole; each of the
     // remaining `tail` tiles runs as two workgroups over the two halves of k
     // (k-tiles [0, khalf) and [khalf, KT)), the first handing its fp32
-    // accumulators to the second through `part` and a flag.
+    // accumulators to the second through `part` and a pair of counts.
     int full, tail, khalf;
     uint32_t* part;      // [tail][8 waves][32][64 lanes] x 16 bytes
-    unsigned* flags;     // [tail], zero between calls
+    unsigned* flags;     // [tail][produced, consumed], equal between calls
+    int tail_polls;      // bound of the second half's wait
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const uint16_t* base, int64_t bytes) {
@@ -214,12 +215,18 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
 
     // ---- tail hand-over: the first half stores its accumulators
     // (device-coherent 16-byte stores, lane-contiguous) and, once every
-    // wave's stores have completed, raises the tile's flag; the second half
-    // waits for the flag (bounded: both halves run in the same last round of
-    // workgroups) and adds them.
+    // wave's stores have completed, bumps the tile's produced count; the
+    // second half waits (bounded: both halves run in the same last round of
+    // workgroups) until the produced count is ahead of its own consumed
+    // count, adds them and bumps the consumed count.  The two counts only
+    // grow and each has one writer, so a hand-over that gave up (recorded in
+    // the error word; the output then lacks the first half) is absorbed: the
+    // late producer's bump evens the counts, and the next call waits for its
+    // own producer again.
     if (is_tail) {
         uint32_t* pt = p.part + ((static_cast<int64_t>(tj >> 1) * 8 + wave) * 32) * 64 * 4;
-        unsigned* flag = p.flags + (tj >> 1);
+        unsigned* produced = p.flags + 2 * (tj >> 1);
+        unsigned* consumed = produced + 1;
         if (!half) {
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib)
@@ -233,30 +240,50 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
                         for (int e = 0; e < 4; ++e) v[e] = __float_as_uint(acc[ib][jb][4 * qd + e]);
                         st_coh<4>(pt + rr * 64 * 4, lane * 16, v);
                     }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __syncthreads();
-            if (tid == 0) __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid == 0) __hip_atomic_fetch_add(produced, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
         }
+        // the ready bit travels through the first LDS word once every wave is
+        // done with the operand stages (a separate __shared__ variable would
+        // take the kernel past 144 KB of LDS, measured 12% slower)
+        int& tail_ready = *reinterpret_cast<int*>(lds);
+        lds_barrier();
         if (tid == 0) {
-            for (int it = 0; it < (1 << 22); ++it) {
-                if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
+            const unsigned c = __hip_atomic_load(consumed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            int ready = 0;
+            for (int it = 0;; ++it) {
+                const unsigned pr = __hip_atomic_load(produced, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (static_cast<int>(pr - c) > 0) {
+                    ready = 1;
+                    break;
+                }
+                if (it >= p.tail_polls) {
+                    wait_expired(kWaitGemmTail);
+                    break;
+                }
                 __builtin_amdgcn_s_sleep(2);
             }
-            __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+            __hip_atomic_store(consumed, c + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            tail_ready = ready;
         }
         __syncthreads();
+        if (tail_ready) {
 #pragma unroll
-        for (int ib = 0; ib < 4; ++ib)
+            for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-            for (int jb = 0; jb < 2; ++jb)
+                for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-                for (int qd = 0; qd < 4; ++qd) {
-                    const int rr = (ib * 2 + jb) * 4 + qd;
-                    const u32x4_v v = ld_coh<4>(pt + rr * 64 * 4, lane * 16);
+                    for (int qd = 0; qd < 4; ++qd) {
+                        const int rr = (ib * 2 + jb) * 4 + qd;
+                        const u32x4_v v = ld_coh<4>(pt + rr * 64 * 4, lane * 16);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[ib][jb][4 * qd + e] += __uint_as_float(v[e]);
-                }
+                        for (int e = 0; e < 4; ++e) acc[ib][jb][4 * qd + e] += __uint_as_float(v[e]);
+                    }
+        }
     }
 
     // ---- epilogue, through LDS: lane holds column wn 64 + jb 32 + lane % 32
@@ -368,7 +395,9 @@ __global__ void gemm_bt_simple_kernel(GemmKParams p) {
 int gemm_bt(hipStream_t st, const GemmArgs& g) {
     if (g.batch <= 0 || g.m <= 0 || g.k < 0 || g.nseg < 1 || g.nseg > 3) return 1;
     if (g.lda < g.k || g.batch > 65535) return 1;
-    const bool tiled = g.k % 8 == 0 && g.lda % 8 == 0 && g.lda <= (1 << 22);
+    // 32-bit per-lane copy offsets: 256 rows of lda elements stay below the
+    // buffer range (2^31 - 16 bytes)
+    const bool tiled = g.k % 8 == 0 && g.lda % 8 == 0 && g.lda < (1 << 22);
     GemmKParams p{};
     p.a = g.a;
     p.lda = g.lda;
@@ -409,6 +438,7 @@ int gemm_bt(hipStream_t st, const GemmArgs& g) {
             p.tail = tail;
             p.khalf = KT / 2;
             p.flags = static_cast<unsigned*>(g.ws);
+            p.tail_polls = wait_polls(1 << 22);
             p.part = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(g.ws) + kGemmFlagBytes);
         }
     }
@@ -431,5 +461,7 @@ int gemm_bt(hipStream_t st, const GemmArgs& g) {
     }
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
+
+hipError_t take_wait_error_gemm(unsigned* bits) { return take_wait_error(bits); }
 
 }  // namespace ssa

@@ -24,13 +24,13 @@ struct GemmArgs {
     int64_t w_bs = 0, o_bs = 0;  // batch strides (elements) of w and out (segment 0 only when batched)
     int epilogue = kGemmStore;   // residual: out = bf16(out + bf16(a.w^T)), in place (one segment)
     // Optional workspace (zero-filled before its first use; every call leaves
-    // its flags at zero) for splitting the last partial round of tiles along
+    // each tile's two hand-over counts equal) for splitting the last partial round of tiles along
     // k; without one (or too small) the tail runs whole.
     void* ws = nullptr;
     size_t ws_bytes = 0;
 };
 
-constexpr size_t kGemmFlagBytes = 4096;  // tail flags (<= 1024 tail tiles)
+constexpr size_t kGemmFlagBytes = 8192;  // tail counts, two per tile (<= 1024 tail tiles)
 // Workspace bytes of the tail split for `tail` tiles.
 inline size_t gemm_tail_bytes(int tail) { return kGemmFlagBytes + static_cast<size_t>(tail) * 8 * 32 * 64 * 16; }
 // Workspace bytes for the tail split of a GEMM of m rows and the given

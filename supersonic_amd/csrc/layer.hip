@@ -4,7 +4,8 @@
 // kernels/qwen36_moe_persistent/full_attn_phase.cuh:1-20, and the HIP
 // megakernel's steps A-G, kernels/full_attention_4b.hip:4842-5577).
 //
-// One workgroup per compute unit (all of them resident at once), three phases
+// One workgroup per compute unit (all of them resident at once: a cooperative
+// launch), three phases
 // separated by device-wide barriers:
 //   1. input RMSNorm (applied while each workgroup stages the rows in LDS) and
 //      the Q/K/V weight stream, 16 output columns per workgroup task;
@@ -20,6 +21,7 @@
 // kernel.
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -36,6 +38,7 @@ struct LayerParams {
     DecodeParams dec;     // phase 2: fused decode step, ragged plan over the grid
     SkinnyLdsParams op;   // phase 3: attn -> hidden (residual in place)
     unsigned* bar;        // barrier counters [0..2] and flags [32], [48] (another cache line), zero between calls
+    int polls;            // bound of a barrier wait (kLayerSpin)
     // > 0: the decode step is expected to have this many work items (one
     // sequence of length max_kv_len); the last `hint` workgroups then take
     // them and skip phase 1, which the others share.
@@ -55,19 +58,41 @@ constexpr int kLayerSpin = 1 << 20;               // bounded barrier wait
 // last wave's first: it waits for the count to come back, and wave 0 goes on.
 // Split form: arrive (after this workgroup's stores are complete), do
 // independent work, then wait.
+//
+// Ordering: the producer's data stores are sc1 (written through to the
+// device coherence point); `s_waitcnt vmcnt(0)` makes each wave wait until
+// they are acknowledged there, the workgroup barrier orders every wave's wait
+// before the counting atomic, and the compiler fences keep the stores above
+// the wait.  A consumer issues its sc1 loads only after its poll has returned
+// the flag (the poll result is waited for before the branch, and the
+// workgroup barrier after the poll orders the other waves' loads after it),
+// and sc1 loads are served from the coherence point, not from a stale
+// per-XCD cache line.  This is what an agent-scope release / acquire pair
+// provides, without the L2 writeback and invalidate those emit.
+//
+// The launch is cooperative (every workgroup co-resident, or the launch is
+// refused), so a wait can only expire on a workspace whose counters were not
+// zero: it then sets kWaitLayerBarrier in the error word and carries on, so
+// that the kernel still exits.
 constexpr int kArriveThread = kLayerThreads - 64;
 __device__ __forceinline__ void grid_arrive(unsigned* ctr, unsigned* flag, unsigned n) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (threadIdx.x == kArriveThread) {
         const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (prev == n - 1) __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
-__device__ __forceinline__ void grid_wait(unsigned* flag) {
+__device__ __forceinline__ void grid_wait(unsigned* flag, int polls) {
     if (threadIdx.x == 0) {
-        for (int it = 0; it < kLayerSpin; ++it) {
+        for (int it = 0;; ++it) {
             if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
+            if (it >= polls) {
+                wait_expired(kWaitLayerBarrier);
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
     }
@@ -114,7 +139,7 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
     grid_arrive(&P.bar[0], &P.bar[32], nwg);
     bool had_item = false;
     decode_split_body<bf16_t, FP8, D, 4, true>(P.dec, item, 0, 0, lds.d, [&]() {
-        grid_wait(&P.bar[32]);
+        grid_wait(&P.bar[32], P.polls);
         had_item = true;
     });
     if (!had_item && w < ncb_op) {
@@ -134,24 +159,24 @@ __global__ __launch_bounds__(kLayerThreads) void decode_layer_kernel(LayerParams
     // Barrier 1: every workgroup arrives; those with an output-projection
     // task wait for all of them.
     grid_arrive(&P.bar[1], &P.bar[48], nwg);
-    if (w < ncb_op) grid_wait(&P.bar[48]);
-    // every workgroup has arrived at barrier 1, so every reader of barrier 0 is past it
-    if (w == 0 && threadIdx.x == 0) {
-        P.bar[0] = 0u;
-        P.bar[32] = 0u;
-    }
+    if (w < ncb_op) grid_wait(&P.bar[48], P.polls);
     // 3. output projection + residual
     for (int cb = w; cb < ncb_op; cb += nwg) {
         skinny_lds_body<HT, true, false, false, bf16_t, true, false>(P.op, RopeEpi{}, cb, 0, lds.s);
         __syncthreads();
     }
-    // the last workgroup to finish resets the remaining counters
+    // The last workgroup to finish resets every counter and flag: each
+    // workgroup counts itself in here after its last arrival and its last
+    // poll, so nothing reads or bumps them any more in this call, whether or
+    // not a wait gave up.
     if (threadIdx.x == 0) {
         const unsigned prev = __hip_atomic_fetch_add(&P.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (prev == nwg - 1) {
-            P.bar[1] = 0u;
-            P.bar[48] = 0u;
-            P.bar[2] = 0u;
+            __hip_atomic_store(&P.bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&P.bar[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&P.bar[32], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&P.bar[48], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&P.bar[2], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -201,6 +226,11 @@ inline LayerWs layer_ws(int B, int Hq, int Hkv, int D, int max_len) {
     return w;
 }
 
+static bool plain_launch() {
+    const char* v = getenv("SUPERSONIC_LAYER_LAUNCH");
+    return v && std::strcmp(v, "plain") == 0;
+}
+
 template <typename HT, bool FP8, int D>
 static int launch_layer(int device, hipStream_t st, LayerParams& P) {
     const int grid = std::min(layer_grid<HT, FP8, D>(device), kLayerMaxGrid);
@@ -224,9 +254,40 @@ static int launch_layer(int device, hipStream_t st, LayerParams& P) {
         const int64_t items = std::max<int64_t>(1, (l + c - 1) / c) * Hkv;
         if (2 * items <= grid) P.hint = static_cast<int>(items);
     }
-    hipLaunchKernelGGL((decode_layer_kernel<HT, FP8, D>), dim3(grid), dim3(kLayerThreads), 0, st, P);
-    return hipGetLastError() == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
+    P.polls = wait_polls(kLayerSpin);
+    P.dec.merge_polls = wait_polls(kMergePoll);
+    // Cooperative launch: the runtime refuses a grid whose workgroups cannot
+    // all be resident at once, which the barriers need (as the reference's
+    // persistent kernel does, kernels/full_attention_bridge_4b.cpp:4918-4927, :4963).
+    // SUPERSONIC_LAYER_LAUNCH=plain: an ordinary launch (no co-residency
+    // guarantee; a barrier that gives up is reported by the error word).
+    if (plain_launch()) {
+        hipLaunchKernelGGL((decode_layer_kernel<HT, FP8, D>), dim3(grid), dim3(kLayerThreads), 0, st, P);
+        return hipGetLastError() == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
+    }
+    void* args[] = {&P};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_layer_kernel<HT, FP8, D>),
+                                                    dim3(grid), dim3(kLayerThreads), args, 0, st);
+    if (e == hipErrorCooperativeLaunchTooLarge) return SUPERSONIC_ERR_COOPERATIVE;
+    return e == hipSuccess ? 0 : SUPERSONIC_ERR_LAUNCH;
 }
+
+// Whether `device` runs cooperative launches (cached per device).
+static bool cooperative_ok(int device) {
+    static std::mutex mu;
+    static std::vector<int> ok;
+    std::lock_guard<std::mutex> lock(mu);
+    if (device < 0) return false;
+    if (static_cast<size_t>(device) >= ok.size()) ok.resize(device + 1, -1);
+    if (ok[device] < 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess) v = 0;
+        ok[device] = v != 0;
+    }
+    return ok[device] != 0;
+}
+
+hipError_t take_wait_error_layer(unsigned* bits) { return take_wait_error(bits); }
 
 }  // namespace ssa
 
@@ -351,6 +412,7 @@ extern "C" int supersonic_attn_gfx950_decode_layer(
     o.k = static_cast<int>(adim);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int dev = static_cast<int>(device_ordinal);
+    if (!plain_launch() && !cooperative_ok(dev)) return SUPERSONIC_ERR_COOPERATIVE;
     const ProfileEvents ev = take_profile_events();
     if (ev.before) (void)hipEventRecord(ev.before, st);
     int rc;

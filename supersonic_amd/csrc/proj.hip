@@ -27,8 +27,11 @@
 // loading its k range of the rows with the lanes past m masked off (measured:
 // o_proj 13.6 -> 12.6 us, Q/K/V 29.1 -> 26.6 us at the config-2 decode shape).
 //
-// More rows are plain GEMMs and go to hipBLASLt (bf16 in/out, fp32
-// accumulate), followed by the residual kernel where one is asked for.
+// More rows are plain GEMMs and go to the hand-written MFMA GEMM (gemm.hip).
+// SUPERSONIC_PROJ_GEMM=hipblaslt sends them to hipBLASLt instead, for
+// comparison; the library then opens libhipblaslt at run time (dlopen), so the
+// product library does not link it and integrators do not inherit it.
+#include <dlfcn.h>
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdlib>
@@ -466,6 +469,48 @@ int launch_skinny(int dev, hipStream_t st, int batch, SkinnyParams p, uint8_t* w
 // In hipBLASLt's column-major terms that is D (n x m, ld n) = op_T(A: k x n, ld k) . B (k x m, ld k).
 // ---------------------------------------------------------------------------
 namespace {
+// hipBLASLt entry points resolved with dlsym on first use (types from its header only).
+struct LtApi {
+    bool tried = false, ok = false;
+#define SSA_LT_FN(name) decltype(&::name) name = nullptr;
+    SSA_LT_FN(hipblasLtCreate)
+    SSA_LT_FN(hipblasLtMatrixLayoutCreate)
+    SSA_LT_FN(hipblasLtMatrixLayoutSetAttribute)
+    SSA_LT_FN(hipblasLtMatmulDescCreate)
+    SSA_LT_FN(hipblasLtMatmulDescSetAttribute)
+    SSA_LT_FN(hipblasLtMatmulPreferenceCreate)
+    SSA_LT_FN(hipblasLtMatmulPreferenceSetAttribute)
+    SSA_LT_FN(hipblasLtMatmulPreferenceDestroy)
+    SSA_LT_FN(hipblasLtMatmulAlgoGetHeuristic)
+    SSA_LT_FN(hipblasLtMatmul)
+#undef SSA_LT_FN
+    bool load() {
+        if (tried) return ok;
+        tried = true;
+        void* h = dlopen("libhipblaslt.so.1", RTLD_NOW | RTLD_LOCAL);
+        if (!h) h = dlopen("/opt/rocm/lib/libhipblaslt.so.1", RTLD_NOW | RTLD_LOCAL);
+        if (!h) return false;
+        bool all = true;
+#define SSA_LT_SYM(name) \
+    name = reinterpret_cast<decltype(name)>(dlsym(h, #name)); \
+    all = all && name != nullptr;
+        SSA_LT_SYM(hipblasLtCreate)
+        SSA_LT_SYM(hipblasLtMatrixLayoutCreate)
+        SSA_LT_SYM(hipblasLtMatrixLayoutSetAttribute)
+        SSA_LT_SYM(hipblasLtMatmulDescCreate)
+        SSA_LT_SYM(hipblasLtMatmulDescSetAttribute)
+        SSA_LT_SYM(hipblasLtMatmulPreferenceCreate)
+        SSA_LT_SYM(hipblasLtMatmulPreferenceSetAttribute)
+        SSA_LT_SYM(hipblasLtMatmulPreferenceDestroy)
+        SSA_LT_SYM(hipblasLtMatmulAlgoGetHeuristic)
+        SSA_LT_SYM(hipblasLtMatmul)
+#undef SSA_LT_SYM
+        ok = all;
+        return ok;
+    }
+};
+LtApi g_lt_api;  // guarded by g_lt_mutex
+
 struct LtPlan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
@@ -508,7 +553,7 @@ int gemm_segments(int dev, hipStream_t st, int m, int k, const void* a, int nseg
             if (ws_bytes < need) return 1;
             g.ws = ws;
         } else {
-            g.ws = device_workspace(dev, need, kWorkspaceGemm);  // zero-filled once; flags stay zero after a call
+            g.ws = device_workspace(dev, need, kWorkspaceGemm);  // zero-filled once; each call leaves the tail counts equal
         }
         g.ws_bytes = g.ws ? need : 0;
     }
@@ -516,12 +561,12 @@ int gemm_segments(int dev, hipStream_t st, int m, int k, const void* a, int nseg
 }
 
 bool make_layout(hipblasLtMatrixLayout_t* l, uint64_t rows, uint64_t cols, int64_t ld, int batch, int64_t stride) {
-    if (hipblasLtMatrixLayoutCreate(l, HIP_R_16BF, rows, cols, ld) != HIPBLAS_STATUS_SUCCESS) return false;
+    if (g_lt_api.hipblasLtMatrixLayoutCreate(l, HIP_R_16BF, rows, cols, ld) != HIPBLAS_STATUS_SUCCESS) return false;
     if (batch > 1) {
         const int32_t bc = batch;
-        if (hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
+        if (g_lt_api.hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) !=
                 HIPBLAS_STATUS_SUCCESS ||
-            hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &stride,
+            g_lt_api.hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &stride,
                                               sizeof(stride)) != HIPBLAS_STATUS_SUCCESS)
             return false;
     }
@@ -534,8 +579,9 @@ bool make_layout(hipblasLtMatrixLayout_t* l, uint64_t rows, uint64_t cols, int64
 int lt_gemm(int dev, hipStream_t st, int batch, int m, int n, int k, const void* lhs, const void* rhs, void* out,
             void* ws = nullptr) {
     std::lock_guard<std::mutex> lock(g_lt_mutex);
+    if (!g_lt_api.load()) return 1;
     LtDevice& D = g_lt[dev];
-    if (!D.handle && hipblasLtCreate(&D.handle) != HIPBLAS_STATUS_SUCCESS) {
+    if (!D.handle && g_lt_api.hipblasLtCreate(&D.handle) != HIPBLAS_STATUS_SUCCESS) {
         D.handle = nullptr;
         return 1;
     }
@@ -546,31 +592,31 @@ int lt_gemm(int dev, hipStream_t st, int batch, int m, int n, int k, const void*
     if (it == D.plans.end()) {
         LtPlan P;
         const hipblasOperation_t opA = HIPBLAS_OP_T, opB = HIPBLAS_OP_N;
-        if (hipblasLtMatmulDescCreate(&P.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
-            hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opA, sizeof(opA)) !=
+        if (g_lt_api.hipblasLtMatmulDescCreate(&P.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+            g_lt_api.hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opA, sizeof(opA)) !=
                 HIPBLAS_STATUS_SUCCESS ||
-            hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opB, sizeof(opB)) !=
+            g_lt_api.hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opB, sizeof(opB)) !=
                 HIPBLAS_STATUS_SUCCESS ||
             !make_layout(&P.a, k, n, k, batch, static_cast<int64_t>(n) * k) ||
             !make_layout(&P.b, k, m, k, batch, static_cast<int64_t>(m) * k) ||
             !make_layout(&P.d, n, m, n, batch, static_cast<int64_t>(m) * n))
             return 1;
         hipblasLtMatmulPreference_t pref;
-        if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return 1;
+        if (g_lt_api.hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return 1;
         const uint64_t wsb = kLtWorkspace;
-        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
+        g_lt_api.hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
         hipblasLtMatmulHeuristicResult_t res[1];
         int found = 0;
         const hipblasStatus_t hs =
-            hipblasLtMatmulAlgoGetHeuristic(D.handle, P.desc, P.a, P.b, P.d, P.d, pref, 1, res, &found);
-        hipblasLtMatmulPreferenceDestroy(pref);
+            g_lt_api.hipblasLtMatmulAlgoGetHeuristic(D.handle, P.desc, P.a, P.b, P.d, P.d, pref, 1, res, &found);
+        g_lt_api.hipblasLtMatmulPreferenceDestroy(pref);
         if (hs != HIPBLAS_STATUS_SUCCESS || found < 1) return 1;
         P.algo = res[0].algo;
         it = D.plans.emplace(key, P).first;
     }
     const LtPlan& P = it->second;
     const float alpha = 1.f, beta = 0.f;
-    if (hipblasLtMatmul(D.handle, P.desc, &alpha, rhs, P.a, lhs, P.b, &beta, out, P.d, out, P.d, &P.algo, ws,
+    if (g_lt_api.hipblasLtMatmul(D.handle, P.desc, &alpha, rhs, P.a, lhs, P.b, &beta, out, P.d, out, P.d, &P.algo, ws,
                         kLtWorkspace, st) != HIPBLAS_STATUS_SUCCESS)
         return 2;
     return 0;

@@ -85,6 +85,21 @@ extern "C" void supersonic_attn_gfx950_set_profile_events(void* before, void* af
     ssa::g_prof.after = static_cast<hipEvent_t>(after);
 }
 
+// Waits for `stream`, then reads and clears the error words of the code
+// objects that hold bounded waits on this device.
+extern "C" int supersonic_attn_gfx950_wait_status(size_t device_ordinal, void* stream, uint32_t* bits) {
+    if (!bits) return SUPERSONIC_ERR_NULL;
+    *bits = 0;
+    ssa::ScopedDevice scoped(static_cast<int>(device_ordinal));
+    if (hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess) return SUPERSONIC_ERR_SYNC;
+    unsigned v = 0;
+    if (ssa::take_wait_error_decode(&v) != hipSuccess || ssa::take_wait_error_layer(&v) != hipSuccess ||
+        ssa::take_wait_error_gemm(&v) != hipSuccess)
+        return SUPERSONIC_ERR_SYNC;
+    *bits = v;
+    return 0;
+}
+
 extern "C" const char* supersonic_attn_version(void) { return "supersonic-attn-gfx950 0.1.0"; }
 
 // RoPE tables on the host, RotaryTables::build (crates/qwen35/src/rotary.rs:15-46):

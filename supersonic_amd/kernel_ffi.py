@@ -45,7 +45,11 @@ KV_FP8_E4M3 = 3
 ERR = {
     "DTYPE": 1001, "HEAD_DIM": 1002, "HEADS": 1003, "NULL": 1004, "ROTARY": 1005,
     "WORKSPACE": 1006, "LAUNCH": 1007, "SYNC": 1008, "RANGE": 1009, "CACHE": 1010,
+    "COOPERATIVE": 1011,
 }
+WAIT_LAYER_BARRIER = 1
+WAIT_DECODE_MERGE = 2
+WAIT_GEMM_TAIL = 4
 
 
 class KvCacheDesc(C.Structure):
@@ -111,6 +115,7 @@ SIGNATURES = {
          _p, C.POINTER(KvCacheDesc), _p, _sz],
     "supersonic_attn_gfx950_quantize_kv_fp8_ocp": [_sz, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "supersonic_attn_gfx950_set_profile_events": [_p, _p],
+    "supersonic_attn_gfx950_wait_status": [_sz, _p, C.POINTER(C.c_uint32)],
     "supersonic_attn_rope_tables": [_sz, _sz, C.c_double, _p, _p],
     "supersonic_attn_version": [],
 }
@@ -461,6 +466,14 @@ def set_profile_events(before, after):
     """Arm the benchmark hook with two torch.cuda.Event (enable_timing=True)."""
     load().supersonic_attn_gfx950_set_profile_events(None if before is None else before.cuda_event,
                                                      None if after is None else after.cuda_event)
+
+
+def wait_status(ordinal=0, stream=None) -> int:
+    """``supersonic_attn_gfx950_wait_status``: synchronise ``stream``, return and
+    clear the SUPERSONIC_WAIT_* bits of bounded waits that gave up since the last call."""
+    bits = C.c_uint32(0)
+    _check("wait_status", load().supersonic_attn_gfx950_wait_status(ordinal, _stream_ptr(stream), C.byref(bits)))
+    return int(bits.value)
 
 
 def rope_tables(rotary_dim, max_pos, theta):

@@ -175,3 +175,29 @@ def test_decode_layer_rejects_unsupported_shapes():
     assert call(8, 8192) == K.ERR["RANGE"]            # rows * hidden > 32768
     assert call(1, 1024, hq=16, hkv=2) == K.ERR["HEADS"]
     assert call(1, 1024, hd=64) == K.ERR["HEAD_DIM"]
+
+
+def test_decode_layer_expired_barrier_is_reported(monkeypatch):
+    """The host presets barrier 0's counter so that its flag is never raised and
+    shortens the poll bound: every wait on it gives up after a few polls (the
+    kernel still exits normally), the error word reports it, every counter and
+    flag is back at zero, and the next call on the same workspace is correct
+    and reports nothing."""
+    c = layer_case(133, B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[2048])
+    ws = torch.zeros(K.decode_layer_workspace_size(c["B"], c["hid"], c["Hq"], c["Hkv"], c["D"], max(c["lens"]) + 1),
+                     dtype=torch.uint8, device=DEV)
+    assert K.wait_status() == 0
+    ws[:4].view(torch.int32).fill_(0x40000000)  # barrier 0 counter: the arrivals never reach the grid size
+    monkeypatch.setenv("SUPERSONIC_WAIT_POLLS", "16")
+    announce("persistent decode layer with barrier 0 held (forced give-up)")
+    run_layer(c, ws)
+    bits = K.wait_status()
+    assert bits & K.WAIT_LAYER_BARRIER, bits
+    assert int(ws[:256].count_nonzero()) == 0, "counters not reset after a wait gave up"
+    monkeypatch.delenv("SUPERSONIC_WAIT_POLLS")
+    announce("persistent decode layer after the forced give-up")
+    c = layer_case(134, B=1, Hq=8, Hkv=2, D=256, rot=64, hid=1024, lens=[2048])
+    out, cache = run_layer(c, ws)
+    assert K.wait_status() == 0
+    ref, v_ref = oracle_layer(c)
+    check_layer(c, out, cache, ref, v_ref)

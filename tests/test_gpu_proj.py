@@ -396,3 +396,38 @@ def test_decode_layer_chain_fused_projection():
     d = (h.float().cpu() - rh).abs()
     assert d.max().item() <= 2e-2 * max(1.0, rh.abs().max().item()) and d.mean().item() <= 2e-3, \
         f"chain: max {d.max().item():.3e} mean {d.mean().item():.3e}"
+
+
+def test_gemm_tail_expired_handover_is_reported(monkeypatch):
+    """The host presets one tail tile's consumed count ahead of its produced count,
+    so that tile's second k half never sees its first half, and shortens the
+    poll bound: the wait gives up, the kernel exits normally and the error word
+    reports it.  A normal call on the re-zeroed workspace is then correct,
+    reports nothing and leaves every tile's two counts equal."""
+    rows, hid, nq, nkv = 4096, 1024, 8192, 1024
+    g = gen(88)
+    hidden = O.randn_bf16(g, rows, hid)
+    nw = O.randn_bf16(g, hid, std=0.1)
+    wq, wk, wv = (O.randn_bf16(g, n, hid, std=hid ** -0.5) for n in (nq, nkv, nkv))
+    args = [t.to(DEV) for t in (hidden, nw, wq, wk, wv)]
+    ws = torch.zeros(K.qkv_proj_workspace_size(rows, hid, nq, nkv), dtype=torch.uint8, device=DEV)
+    counts = ws[rows * hid * 2:rows * hid * 2 + 8192].view(torch.int32)  # the GEMM's region follows the normed rows
+    outs = [torch.empty((rows, w.shape[0]), dtype=torch.bfloat16, device=DEV) for w in (wq, wk, wv)]
+    assert K.wait_status() == 0
+    counts[1] = 1  # tile 0: consumed 1, produced 0
+    monkeypatch.setenv("SUPERSONIC_WAIT_POLLS", "16")
+    announce("qkv_proj tail hand-over held (forced give-up)")
+    K.qkv_proj(0, *args, *outs, workspace=ws)
+    assert K.wait_status() & K.WAIT_GEMM_TAIL
+    monkeypatch.delenv("SUPERSONIC_WAIT_POLLS")
+    ws.zero_()
+    announce("qkv_proj after the forced give-up")
+    K.qkv_proj(0, *args, *outs, workspace=ws)
+    assert K.wait_status() == 0
+    c = counts.cpu().view(-1, 2)
+    assert bool((c[:, 0] == c[:, 1]).all()) and int(c[:, 0].max()) == 1
+    refs = O.qkv_proj(hidden.float(), nw, wq, wk, wv)
+    for name, out, ref in zip("qkv", outs, refs):
+        out = out.cpu()
+        big = torch.maximum(out.float().abs(), ref.float().abs())
+        assert_ulps(out, ref, 2 * ulp(big) + 2.0 ** -8, f"qkv after give-up {name}")
