@@ -61,8 +61,11 @@ extern "C" {
  * bound at crates/kernel-ffi/src/prefill_ffi.rs:899-915.
  * query [B, Hq, q_len, D], key/value [B, Hkv, kv_len, D] (dtype), out f32
  * [B, Hq, q_len, D].  Row p attends keys t < min(kv_len, seqlen_offset + p + 1).
- * dtype 0/1/2.  Status: 64 bad dtype, 14 unsupported head_dim (D > 512 or not
- * a multiple of 8), 2 workspace allocation, 11 launch, 12 sync. */
+ * dtype 0/1/2, any head_dim 1..512 (as the reference on wave64): 64, 128 and
+ * 256 run the MFMA kernel directly, other sizes up to 256 run it on copies
+ * zero-padded to the next of those, larger ones the f32 kernel on f32 copies.
+ * Status: 64 bad dtype, 14 unsupported head_dim (0 or > 512) or heads,
+ * 2 workspace allocation, 11 launch, 12 sync. */
 int supersonic_qwen35_hip_full_attention_prefill(
     int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
     size_t q_len, size_t kv_len, size_t head_dim, size_t num_kv_groups, float scale,
@@ -77,7 +80,11 @@ int supersonic_qwen35_4b_hip_full_attention_prefill(
 /* Single-token decode attention.  Replaces kernels/prefill_helpers_bridge.cpp:444-470
  * (kernel prefill_helpers.hip:319-404), bound at prefill_ffi.rs:917-931.
  * query [B, Hq, D], key/value [B, Hkv, kv_len, D], out [B, Hq*D] (dtype).
- * dtype 0/2.  Status: 400 bad dtype, 401 head_dim > 256, 402 launch, 403 sync. */
+ * dtype 0/2, any head_dim 1..256 and Hq = Hkv * num_kv_groups: head_dim 64,
+ * 128, 256 with up to 16 groups run the split-K kernel directly, other head
+ * sizes on copies zero-padded to the next of those, more groups as a one-row
+ * f32 prefill.  Status: 400 bad dtype, 401 head_dim 0 or > 256 (or heads),
+ * 402 launch or allocation, 403 sync (or a split merge that gave up). */
 int supersonic_qwen35_hip_full_attention_decode_flat(
     int dtype, size_t device_ordinal, size_t batch_size, size_t q_heads, size_t kv_heads,
     size_t kv_len, size_t head_dim, size_t num_kv_groups, float scale,

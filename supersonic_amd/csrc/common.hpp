@@ -328,6 +328,27 @@ hipError_t take_wait_error_decode(unsigned* bits);
 hipError_t take_wait_error_layer(unsigned* bits);
 hipError_t take_wait_error_gemm(unsigned* bits);
 
+// Row repack with cast and zero padding (elementwise.hip): dst row
+// (o, i) of dout elements = src[o * so + i * si + 0 .. din) cast from dtype
+// code tin to tout (0 f16, 1 f32, 2 bf16), zero past din.  Asynchronous on st.
+hipError_t repack_rows(int tin, int tout, const void* src, void* dst, int64_t n_outer, int64_t n_inner, int64_t so,
+                       int64_t si, int din, int dout, hipStream_t st);
+
+// Device buffers of one drop-in call (released when it returns).
+struct ScratchBuffers {
+    void* p[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    int n = 0;
+    void* get(size_t bytes) {
+        void* q = nullptr;
+        if (n >= 6 || hipMalloc(&q, bytes ? bytes : 16) != hipSuccess) return nullptr;
+        p[n++] = q;
+        return q;
+    }
+    ~ScratchBuffers() {
+        for (int i = 0; i < n; ++i) (void)hipFree(p[i]);
+    }
+};
+
 inline unsigned grid1d(size_t n, int block) {
     return static_cast<unsigned>((n + block - 1) / block);
 }

@@ -240,12 +240,60 @@ static const int32_t* uniform_lens(int device, int B, int kv_len, hipStream_t st
     return bufs[device];
 }
 
+int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t Hkv, size_t q_len, size_t kv_len, size_t D,
+                   size_t groups, float scale, size_t off, const void* q, const void* k, const void* v, void* out);
+
 static int decode_flat_common(int dtype, size_t device, size_t B, size_t Hq, size_t Hkv, size_t kv_len,
                               size_t kv_stride, size_t D, size_t groups, float scale, const void* q,
                               const void* k, const void* v, void* out) {
     if (dtype != 0 && dtype != 2) return 400;
-    if (D > 256 || (D != 64 && D != 128 && D != 256)) return 401;
-    if (Hkv == 0 || groups == 0 || Hq != Hkv * groups || groups > 16) return 401;
+    if (D == 0 || D > 256) return 401;
+    if (Hkv == 0 || groups == 0 || Hq != Hkv * groups) return 401;
+    if ((D != 64 && D != 128 && D != 256) || groups > 16) {
+        // General shape (the reference takes any D <= 256 and any group
+        // size): with at most 16 query heads per kv head, the split-K kernel
+        // on copies zero-padded to the next native head size (zero dims add
+        // nothing to q.k; the padded output dims are dropped); with more, the
+        // f32 prefill kernel as a one-row prefill over all kv_len keys.
+        ScopedDevice scoped(static_cast<int>(device));
+        if (B == 0 || Hq == 0) return hipDeviceSynchronize() == hipSuccess ? 0 : 403;
+        const int64_t nq = static_cast<int64_t>(B * Hq), nkv = static_cast<int64_t>(B * Hkv);
+        const int64_t nk = nkv * static_cast<int64_t>(kv_len);
+        const int d = static_cast<int>(D);
+        const int64_t so = static_cast<int64_t>(kv_stride) * d;  // source (sequence, kv head) stride
+        ScratchBuffers sb;
+        int rc;
+        if (groups <= 16) {
+            const int dp = D <= 64 ? 64 : (D <= 128 ? 128 : 256);
+            void* qp = sb.get(nq * dp * 2);
+            void* kp = sb.get(nk * dp * 2);
+            void* vp = sb.get(nk * dp * 2);
+            void* op = sb.get(nq * dp * 2);
+            if (!qp || !kp || !vp || !op) return 402;
+            if (repack_rows(dtype, dtype, q, qp, nq, 1, d, 0, d, dp, nullptr) != hipSuccess ||
+                repack_rows(dtype, dtype, k, kp, nkv, kv_len, so, d, d, dp, nullptr) != hipSuccess ||
+                repack_rows(dtype, dtype, v, vp, nkv, kv_len, so, d, d, dp, nullptr) != hipSuccess)
+                return 402;
+            rc = decode_flat_common(dtype, device, B, Hq, Hkv, kv_len, kv_len, dp, groups, scale, qp, kp, vp, op);
+            if (rc == 0 && repack_rows(dtype, dtype, op, out, nq, 1, dp, 0, d, d, nullptr) != hipSuccess) rc = 402;
+        } else {
+            void* qf = sb.get(nq * d * 4);
+            void* kf = sb.get(nk * d * 4);
+            void* vf = sb.get(nk * d * 4);
+            void* of = sb.get(nq * d * 4);
+            if (!qf || !kf || !vf || !of) return 402;
+            if (repack_rows(dtype, 1, q, qf, nq, 1, d, 0, d, d, nullptr) != hipSuccess ||
+                repack_rows(dtype, 1, k, kf, nkv, kv_len, so, d, d, d, nullptr) != hipSuccess ||
+                repack_rows(dtype, 1, v, vf, nkv, kv_len, so, d, d, d, nullptr) != hipSuccess)
+                return 402;
+            rc = prefill_dropin(1, device, B, Hq, Hkv, 1, kv_len, D, groups, scale, kv_len > 0 ? kv_len - 1 : 0, qf,
+                                kf, vf, of);
+            rc = rc == 0 ? 0 : (rc == 12 ? 403 : 402);
+            if (rc == 0 && repack_rows(1, dtype, of, out, nq, 1, d, 0, d, d, nullptr) != hipSuccess) rc = 402;
+        }
+        if (hipDeviceSynchronize() != hipSuccess && rc == 0) rc = 403;
+        return rc;
+    }
     ScopedDevice scoped(static_cast<int>(device));
     const int dev = static_cast<int>(device);
     const int32_t* lens = uniform_lens(dev, static_cast<int>(B), static_cast<int>(kv_len), nullptr, 0);

@@ -160,6 +160,56 @@ __global__ __launch_bounds__(256) void quantize_kv_kernel(const uint16_t* src, u
     }
 }
 
+// ---------------------------------------------------------------- row repack
+// dst row r = (o, i), o < n_outer, i < n_inner, holds dout elements: the
+// first din come from src[o * so + i * si + c] (cast I -> O), the rest are
+// zero.  The general head-size paths of the drop-ins pad head dims to a
+// native tile (or cast to f32) and compact the results back with it.
+template <typename I, typename O>
+__global__ __launch_bounds__(256) void repack_rows_kernel(const I* src, O* dst, int64_t n_inner, int64_t so,
+                                                          int64_t si, int din, int dout, int64_t total) {
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t r = e / dout;
+        const int c = static_cast<int>(e - r * dout);
+        const int64_t o = r / n_inner, i = r - o * n_inner;
+        store_f32(dst, e, c < din ? load_f32(src, o * so + i * si + c) : 0.f);
+    }
+}
+
+template <typename I, typename O>
+static hipError_t repack_as(const void* src, void* dst, int64_t n_outer, int64_t n_inner, int64_t so, int64_t si,
+                            int din, int dout, hipStream_t st) {
+    const int64_t total = n_outer * n_inner * dout;
+    if (total <= 0) return hipSuccess;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL((repack_rows_kernel<I, O>), dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),
+                       dim3(256), 0, st, static_cast<const I*>(src), static_cast<O*>(dst), n_inner, so, si, din, dout,
+                       total);
+    return hipGetLastError();
+}
+
+template <typename I>
+static hipError_t repack_to(int tout, const void* src, void* dst, int64_t n_outer, int64_t n_inner, int64_t so,
+                            int64_t si, int din, int dout, hipStream_t st) {
+    switch (tout) {
+    case 0: return repack_as<I, f16_t>(src, dst, n_outer, n_inner, so, si, din, dout, st);
+    case 1: return repack_as<I, float>(src, dst, n_outer, n_inner, so, si, din, dout, st);
+    case 2: return repack_as<I, bf16_t>(src, dst, n_outer, n_inner, so, si, din, dout, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t repack_rows(int tin, int tout, const void* src, void* dst, int64_t n_outer, int64_t n_inner, int64_t so,
+                       int64_t si, int din, int dout, hipStream_t st) {
+    switch (tin) {
+    case 0: return repack_to<f16_t>(tout, src, dst, n_outer, n_inner, so, si, din, dout, st);
+    case 1: return repack_to<float>(tout, src, dst, n_outer, n_inner, so, si, din, dout, st);
+    case 2: return repack_to<bf16_t>(tout, src, dst, n_outer, n_inner, so, si, din, dout, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace ssa
 
 using namespace ssa;

@@ -877,12 +877,48 @@ static float rescale_slack() {
     return (v && *v) ? static_cast<float>(atof(v)) : 8.0f;
 }
 
-static int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t Hkv, size_t q_len, size_t kv_len,
-                          size_t D, size_t groups, float scale, size_t off, const void* q, const void* k,
-                          const void* v, void* out) {
+int prefill_dropin(int dtype, size_t device, size_t B, size_t Hq, size_t Hkv, size_t q_len, size_t kv_len, size_t D,
+                   size_t groups, float scale, size_t off, const void* q, const void* k, const void* v, void* out) {
     if (dtype != 0 && dtype != 1 && dtype != 2) return 64;
     if (D == 0 || D > 512 || Hkv == 0 || groups == 0 || Hq != Hkv * groups) return 14;
-    if (dtype != 1 && D != 64 && D != 128 && D != 256) return 14;
+    if (dtype != 1 && D != 64 && D != 128 && D != 256) {
+        // General head size (the reference takes any D <= 512): D <= 256 runs
+        // the MFMA kernel on copies zero-padded to the next native tile (the
+        // zero dims add nothing to q.k, and the padded output dims are dropped);
+        // larger D runs the f32 kernel on f32 copies.
+        ScopedDevice scoped(static_cast<int>(device));
+        if (B == 0 || Hq == 0 || q_len == 0) return hipDeviceSynchronize() == hipSuccess ? 0 : 12;
+        const int64_t nq = static_cast<int64_t>(B * Hq * q_len), nk = static_cast<int64_t>(B * Hkv * kv_len);
+        const int d = static_cast<int>(D);
+        ScratchBuffers sb;
+        int rc;
+        if (D <= 256) {
+            const int dp = D <= 64 ? 64 : (D <= 128 ? 128 : 256);
+            void* qp = sb.get(nq * dp * 2);
+            void* kp = sb.get(nk * dp * 2);
+            void* vp = sb.get(nk * dp * 2);
+            void* op = sb.get(nq * dp * 4);
+            if (!qp || !kp || !vp || !op) return 2;
+            if (repack_rows(dtype, dtype, q, qp, nq, 1, d, 0, d, dp, nullptr) != hipSuccess ||
+                repack_rows(dtype, dtype, k, kp, nk, 1, d, 0, d, dp, nullptr) != hipSuccess ||
+                repack_rows(dtype, dtype, v, vp, nk, 1, d, 0, d, dp, nullptr) != hipSuccess)
+                return 11;
+            rc = prefill_dropin(dtype, device, B, Hq, Hkv, q_len, kv_len, dp, groups, scale, off, qp, kp, vp, op);
+            if (rc == 0 && repack_rows(1, 1, op, out, nq, 1, dp, 0, d, d, nullptr) != hipSuccess) rc = 11;
+        } else {
+            void* qf = sb.get(nq * d * 4);
+            void* kf = sb.get(nk * d * 4);
+            void* vf = sb.get(nk * d * 4);
+            if (!qf || !kf || !vf) return 2;
+            if (repack_rows(dtype, 1, q, qf, nq, 1, d, 0, d, d, nullptr) != hipSuccess ||
+                repack_rows(dtype, 1, k, kf, nk, 1, d, 0, d, d, nullptr) != hipSuccess ||
+                repack_rows(dtype, 1, v, vf, nk, 1, d, 0, d, d, nullptr) != hipSuccess)
+                return 11;
+            rc = prefill_dropin(1, device, B, Hq, Hkv, q_len, kv_len, D, groups, scale, off, qf, kf, vf, out);
+        }
+        if (hipDeviceSynchronize() != hipSuccess && rc == 0) rc = 12;
+        return rc;
+    }
     ScopedDevice scoped(static_cast<int>(device));
     if (B == 0 || Hq == 0 || q_len == 0) return hipDeviceSynchronize() == hipSuccess ? 0 : 12;
     if (dtype == 1) {

@@ -59,7 +59,7 @@ def test_version(lib):
 
 @pytest.mark.parametrize("fn,args,code", [
     ("supersonic_qwen35_hip_full_attention_prefill", (9, 0, 1, 1, 1, 1, 1, 64, 1, 1.0, 0, None, None, None, None), 64),
-    ("supersonic_qwen35_hip_full_attention_prefill", (2, 0, 1, 1, 1, 1, 1, 96, 1, 1.0, 0, None, None, None, None), 14),
+    ("supersonic_qwen35_hip_full_attention_prefill", (2, 0, 1, 1, 1, 1, 1, 0, 1, 1.0, 0, None, None, None, None), 14),
     ("supersonic_qwen35_hip_full_attention_prefill", (2, 0, 1, 1, 1, 1, 1, 1024, 1, 1.0, 0, None, None, None, None), 14),
     ("supersonic_qwen35_hip_full_attention_decode_flat", (1, 0, 1, 1, 1, 1, 256, 1, 1.0, None, None, None, None), 400),
     ("supersonic_qwen35_hip_full_attention_decode_flat", (2, 0, 1, 1, 1, 1, 512, 1, 1.0, None, None, None, None), 401),

@@ -68,6 +68,38 @@ def test_decode_flat_matches_oracle(dtype, B, Hq, Hkv, D, L):
     check(out, ref, TOL_BF16, "decode_flat")
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,D,L", [(2, 8, 2, 80, 1500), (1, 16, 4, 96, 333), (2, 8, 2, 192, 2049),
+                                         (1, 4, 4, 40, 7), (1, 32, 1, 128, 600), (1, 40, 2, 72, 300)])
+def test_decode_flat_general_head_sizes(B, Hq, Hkv, D, L):
+    """Head sizes other than 64/128/256 (zero-padded copies) and more than 16
+    query heads per kv head (one-row f32 prefill), as the reference's decode_flat
+    takes any head_dim <= 256 (prefill_helpers_bridge.cpp:248-275)."""
+    announce(f"decode_flat general B={B} Hq={Hq} Hkv={Hkv} D={D} L={L}")
+    g = gen(14)
+    q = O.randn_bf16(g, B, Hq, D)
+    k = O.randn_bf16(g, B, Hkv, L, D)
+    v = O.randn_bf16(g, B, Hkv, L, D)
+    out = torch.full((B, Hq * D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    K.full_attention_decode_flat(0, K.ScalarType.BF16, B, Hq, Hkv, L, D, D ** -0.5, q.to(DEV), k.to(DEV), v.to(DEV),
+                                 out)
+    ref = O.attention_decode(q, k, v, L, D ** -0.5).reshape(B, Hq * D)
+    check(out, ref, TOL_BF16, f"decode_flat D={D}")
+
+
+def test_decode_flat_general_strided():
+    announce("decode_flat_strided general D=96")
+    B, Hq, Hkv, D, L, cap = 2, 8, 2, 96, 700, 900
+    g = gen(15)
+    q = O.randn_bf16(g, B, Hq, D)
+    k = O.randn_bf16(g, B, Hkv, cap, D)
+    v = O.randn_bf16(g, B, Hkv, cap, D)
+    out = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    K.full_attention_decode_flat_strided(0, K.ScalarType.BF16, B, Hq, Hkv, L, cap, D, D ** -0.5, q.to(DEV),
+                                         k.to(DEV), v.to(DEV), out)
+    ref = O.attention_decode(q, k, v, L, D ** -0.5).reshape(B, Hq * D)
+    check(out, ref, TOL_BF16, "strided general")
+
+
 def test_decode_flat_strided_cache():
     announce("decode_flat_strided")
     B, Hq, Hkv, D, L, cap = 2, 8, 2, 256, 1000, 1280

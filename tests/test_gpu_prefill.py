@@ -53,6 +53,27 @@ def test_prefill_dropin_matches_oracle(dtype, B, Hq, Hkv, S, off, D):
     check(out, ref, TOL_BF16 if dtype != K.ScalarType.F32 else (1e-4, 1e-5), "prefill")
 
 
+@pytest.mark.parametrize("dtype", [K.ScalarType.BF16, K.ScalarType.F16])
+@pytest.mark.parametrize("B,Hq,Hkv,S,off,D", [
+    (1, 4, 2, 300, 0, 80), (2, 8, 2, 129, 40, 96), (1, 16, 4, 200, 100, 192), (1, 2, 1, 70, 3, 36),
+    (1, 4, 2, 65, 10, 320), (1, 2, 2, 33, 0, 512), (1, 2, 1, 17, 4, 500),
+])
+def test_prefill_dropin_general_head_sizes(dtype, B, Hq, Hkv, S, off, D):
+    """Head sizes other than 64/128/256, up to 512, as the reference's prefill
+    takes any head_dim <= 8 x wave size (full_attention_bridge.cpp:86-88):
+    zero-padded copies on the MFMA kernel up to 256, the f32 kernel above."""
+    announce(f"prefill dropin general dtype={dtype} B={B} Hq={Hq} Hkv={Hkv} S={S} off={off} D={D}")
+    tdt = torch.bfloat16 if dtype == K.ScalarType.BF16 else torch.float16
+    g = gen(63)
+    L = off + S
+    q = torch.randn(B, Hq, S, D, generator=g).to(tdt)
+    k = torch.randn(B, Hkv, L, D, generator=g).to(tdt)
+    v = torch.randn(B, Hkv, L, D, generator=g).to(tdt)
+    out = dropin(q, k, v, off, dtype)
+    ref = O.attention_prefill(q.float(), k.float(), v.float(), D ** -0.5, off)
+    check(out, ref, TOL_BF16, f"prefill D={D}")
+
+
 def test_prefill_kv_shorter_than_causal_limit():
     """kv_len < seqlen_offset + q_len: every row is clamped to kv_len keys."""
     announce("prefill clamp")
@@ -191,3 +212,38 @@ def test_fused_prefill_fp8_cache(S, Hq, Hkv, D, rot, start):
     kd = deq(gk, gks) - kch
     assert kd.abs().max().item() <= 2 ** -3 * kch.abs().amax(-1).max().item()
     assert torch.equal(cache.k[0, :, :start].cpu(), pk)  # the prefix is untouched
+
+
+def test_fused_prefill_fp8_full_size():
+    """The fp8-KV lane at the bench shape: a 4096-token chunk after a 4096-token
+    OCP e4m3 prefix, 16/4 heads, D 256.  The oracle covers three blocks of 128
+    query rows (the first, the middle and the last of the chunk, each over its
+    whole causal key range of up to 8192 keys) for every head; the bar is the
+    bf16 one, since the prefix enters both sides dequantised the same way."""
+    S, start, Hq, Hkv, D, rot = 4096, 4096, 16, 4, 256, 64
+    announce(f"fused prefill fp8 full size S={S} start={start}")
+    c = fused_case(75, S, Hq, Hkv, D, rot, start)
+    cap = start + S
+    pk, pks = fp8_rows(c["prefix_k"])
+    pv, pvs = fp8_rows(c["prefix_v"])
+    kq = torch.zeros(1, Hkv, cap, D, dtype=torch.uint8)
+    vq = torch.zeros_like(kq)
+    ks = torch.zeros(1, Hkv, cap, dtype=torch.float32)
+    vs = torch.zeros_like(ks)
+    kq[0, :, :start], ks[0, :, :start] = pk, pks
+    vq[0, :, :start], vs[0, :, :start] = pv, pvs
+    cache = K.KvCache(kq.to(DEV), vq.to(DEV), ks.to(DEV), vs.to(DEV))
+    out = run_fused_prefill(c, start, cache).float().cpu()
+    deq = lambda q, sc: (torch.from_numpy(fp8_codec.decode(q.numpy())) * sc[..., None]).bfloat16().float()
+    sh = c["shape"]
+    pos = torch.arange(start, start + S)
+    q, gate, k = O.prep_qk(sh, c["q_proj"], c["k_new"], c["qw"], c["kw"], c["cos"], c["sin"], pos)
+    v = O.bf16r(c["v_new"].float()).reshape(S, Hkv, D)
+    k_all = torch.cat([deq(pk, pks), k.permute(1, 0, 2)], dim=1)[None]
+    v_all = torch.cat([deq(pv, pvs), v.permute(1, 0, 2)], dim=1)[None]
+    torch.set_num_threads(max(1, os.cpu_count() or 1))
+    for r0 in (0, S // 2, S - 128):
+        qb = q[r0:r0 + 128].permute(1, 0, 2)[None]
+        attn = O.attention_prefill(qb, k_all, v_all, sh.scale, start + r0)[0]
+        ref = O.sigmoid_mul(O.bf16r(attn).permute(1, 0, 2), gate[r0:r0 + 128]).reshape(128, Hq * D)
+        check(out[r0:r0 + 128], ref, TOL_BF16, f"fp8 prefill rows {r0}..{r0 + 127}")
