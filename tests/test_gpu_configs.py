@@ -33,6 +33,8 @@ def gpu_randn(seed, *shape):
 
 def fused_decode(case_dev, cache, B, Hq, Hkv, D, rot, max_len, stream=None):
     out = torch.full((B, Hq * D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    if stream is not None:
+        stream.wait_stream(torch.cuda.current_stream())  # the fill above runs on the current stream
     K.fused_decode(0, case_dev["q_proj"], case_dev["k_new"], case_dev["v_new"], case_dev["qw"], case_dev["kw"],
                    case_dev["cos"], case_dev["sin"], case_dev["pos"], cache, out, q_heads=Hq, kv_heads=Hkv,
                    head_dim=D, rotary_dim=rot, max_kv_len=max_len, stream=stream)
