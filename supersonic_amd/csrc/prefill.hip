@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     typedef Tile<D> T;
     constexpr int KS = D / 32;        // QK^T k-steps (32 dims each)
     constexpr int DBK = D / 16;       // 16-dim output blocks
-    // [stage][K | V] tiles; stage 0 also holds the query rows in the prologue
+    // [stage][K | V] tiles; the fused prologue stages the query rows in one stage
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * T::STAGE];
 
     const int tid = threadIdx.x;
@@ -231,11 +231,98 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const int W = by_xcd ? (p.n_wg >> 3) : p.n_wg;
     const int hpi = by_xcd ? hpx : p.Hq;     // heads per item list
     const int n_items = p.nqt * hpi * p.B;
+    // Item r of this workgroup (false past the last): 128 query rows `qt` of
+    // head h of sequence b.  The sequence of m is increasing.
+    auto item_at = [&](const int r, int& qt, int& h, int& b) -> bool {
+        const int m = (r & 1) ? (r + 1) * W - 1 - j : r * W + j;
+        if (m >= n_items) return false;
+        qt = p.nqt - 1 - m / (hpi * p.B);
+        const int rem = m % (hpi * p.B);
+        h = (by_xcd ? (bid & 7) * hpx : 0) + rem % hpi;
+        b = rem / hpi;
+        return true;
+    };
+    // 64-key tiles of query block qt: keys below the block's last row (causal).
+    auto tiles_of = [&](const int qt) -> int {
+        const int lim = min(p.L, p.off + min(qt * 128 + 128, p.S));
+        return lim > 0 ? (lim + 63) / 64 : 0;
+    };
+    // Tiles alternate between the two LDS stages across items: tile `it` of
+    // an item that follows gt tiles goes to stage (gt + it + 1) & 1, so the
+    // next item's first tile can be copied while this item's last tile is
+    // computed, and the fused query staging of an item uses stage gt & 1 (its
+    // previous item's last tile, read by then).
+    //
+    // Copy waves: the next tile is issued once every wave has passed the
+    // barrier of tile it (the stage it goes to was last read by tile it - 1)
+    // and has landed by the next barrier.  Same barrier count per item as the
+    // compute waves (one per tile plus the item end).
+    auto copy_items = [&]() {
+        const int lane = tid & 63;
+        const int dma_lane = (lane / (D / 8)) * T::NR * T::ROWB + (lane % (D / 8)) * 16;
+        const int vt_rowb = 2 * p.vt_ld;
+        const int vt_lane0 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (lane >> 4));
+        const int vt_lane1 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (4 + (lane >> 4)));
+        // Direct global->LDS copy of key tile `it` of (h, b) into stage `st`
+        // (asynchronous, counted by vmcnt).  K: lane l of copy instruction i
+        // moves 16 bytes of row i + NR (l / (D/8)); rows past kv_len fall
+        // outside the buffer range and read as zeros (masked later; never
+        // stale cache contents).  V^T: lane l of instruction i moves chunk
+        // c = (l & 7) ^ (4 (i & 1) + (l >> 4)) of dim 8 i + (l >> 3) (the
+        // swizzle of the tile geometry); the staging buffer is zero past kv_len.
+        auto issue_tile = [&](const int h, const int b, const int it, const int st) {
+            const int kvh = h / p.G;
+            const uint16_t* vt_head = p.vt + (static_cast<int64_t>(b) * p.Hkv + kvh) * D * p.vt_ld;
+            const int k0 = it * 64;
+            const int64_t base = p.kv.row_uniform(b, kvh, k0, D) * 2;  // a tile lies inside one page
+            const __amdgpu_buffer_rsrc_t kr = tile_rsrc(p.kv.k + base, min(64, p.L - k0) * T::ROWB);
+            const __amdgpu_buffer_rsrc_t vr = tile_rsrc(reinterpret_cast<const uint8_t*>(vt_head + k0),
+                                                        D * vt_rowb - 2 * k0);
+            const int cw = wave - kPrefillWaves;
+            const int lbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + cw * T::NI * T::KBLK);
+            const int vbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + T::KBYTES + cw * T::NI * 1024);
+#pragma unroll
+            for (int jj = 0; jj < T::NI; ++jj) {
+                const int i = cw * T::NI + jj;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)(lds + lbase + jj * T::KBLK),
+                                                         16, dma_lane, i * T::ROWB, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(lds + vbase + jj * 1024),
+                                                         16, (i & 1) ? vt_lane1 : vt_lane0, 8 * i * vt_rowb, 0, 0);
+            }
+        };
+        // s_waitcnt vmcnt(0) alone (the other counters are not waited for)
+        auto wait_vm0 = []() { __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); };
+        // first tile of the first item that has keys at all
+        auto issue_first = [&](int r, const int st) {
+            int qt, h, b;
+            for (; item_at(r, qt, h, b); ++r)
+                if (tiles_of(qt) > 0) {
+                    issue_tile(h, b, 0, st);
+                    return;
+                }
+        };
+        issue_first(0, 1);
+        int gt = 0, qt, h, b;
+        for (int r = 0; item_at(r, qt, h, b); ++r) {
+            const int nt = tiles_of(qt);
+            for (int it = 0; it < nt; ++it) {
+                // Tile `it` has landed.  The compute waves' barrier also
+                // orders their LDS reads; these waves read no LDS, so a bare
+                // barrier (no implied wait for every load in flight) is enough.
+                wait_vm0();
+                __builtin_amdgcn_s_barrier();
+                if (it + 1 < nt) issue_tile(h, b, it + 1, (gt + it + 2) & 1);
+                else issue_first(r + 1, (gt + nt + 1) & 1);
+            }
+            __builtin_amdgcn_s_barrier();  // item end (the next tile needs no wait yet)
+            gt += nt;
+        }
+        wait_vm0();  // no LDS write in flight when the workgroup ends
+    };
     // One work item = 128 query rows of one head of one sequence, run by the
-    // copy waves (COPY) or the compute waves.  A `return` inside ends the
-    // item, not the workgroup.
-    auto run_item = [&](auto copy_tag, const int qt, const int h, const int b) {
-        constexpr bool COPY = decltype(copy_tag)::value;
+    // compute waves; gt = tiles of the workgroup's items before it.  A
+    // `return` inside ends the item, not the workgroup.
+    auto run_item = [&](const int qt, const int h, const int b, const int gt) {
     // Opaque per item, so the compiler does not hoist lane-derived values and
     // loads (norm weights, offsets) out of the item loop, where they would
     // stay live through the key loop.
@@ -249,60 +336,9 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const bool row_ok = myrow < p.S;
     const int S = p.S, L = p.L, off = p.off;
 
-    const int lim_wg = min(L, off + min(q0 + 128, S));
-    const int ntiles = lim_wg > 0 ? (lim_wg + 63) / 64 : 0;
+    const int ntiles = tiles_of(qt);
     const int lim_wave = min(L, off + min(row_w0 + 16, S));
     const int lim_row = min(L, off + myrow + 1);
-
-    // Direct global->LDS copy of key tile `it` into stage `st` (asynchronous,
-    // counted by vmcnt).  K: lane l of copy instruction i moves 16 bytes of
-    // row i + NR (l / (D/8)); rows past kv_len fall outside the buffer range
-    // and read as zeros (masked later; never stale cache contents).  V^T:
-    // lane l of instruction i moves chunk c = (l & 7) ^ (4 (i & 1) + (l >> 4))
-    // of dim 8 i + (l >> 3) (the swizzle of the tile geometry); the staging
-    // buffer is zero past kv_len.
-    const int dma_lane = (lane / (D / 8)) * T::NR * T::ROWB + (lane % (D / 8)) * 16;
-    const int vt_rowb = 2 * p.vt_ld;
-    const int vt_lane0 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (lane >> 4));
-    const int vt_lane1 = (lane >> 3) * vt_rowb + 16 * ((lane & 7) ^ (4 + (lane >> 4)));
-    const uint16_t* vt_head = p.vt + (static_cast<int64_t>(b) * p.Hkv + kvh) * D * p.vt_ld;
-    // Tile it goes to stage (it + 1) & 1.
-    auto issue_tile = [&](int it) {
-        const int k0 = it * 64;
-        const int st = (it + 1) & 1;
-        const int64_t base = p.kv.row_uniform(b, kvh, k0, D) * 2;  // a tile lies inside one page
-        const __amdgpu_buffer_rsrc_t kr = tile_rsrc(p.kv.k + base, min(64, L - k0) * T::ROWB);
-        const __amdgpu_buffer_rsrc_t vr = tile_rsrc(reinterpret_cast<const uint8_t*>(vt_head + k0),
-                                                    D * vt_rowb - 2 * k0);
-        const int cw = wave - kPrefillWaves;
-        const int lbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + cw * T::NI * T::KBLK);
-        const int vbase = __builtin_amdgcn_readfirstlane(st * T::STAGE + T::KBYTES + cw * T::NI * 1024);
-#pragma unroll
-        for (int j = 0; j < T::NI; ++j) {
-            const int i = cw * T::NI + j;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)(lds + lbase + j * T::KBLK),
-                                                     16, dma_lane, i * T::ROWB, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(lds + vbase + j * 1024),
-                                                     16, (i & 1) ? vt_lane1 : vt_lane0, 8 * i * vt_rowb, 0, 0);
-        }
-    };
-    if constexpr (COPY) {
-        // Copy waves: the next tile is issued once everyone has passed the
-        // barrier of tile it (its stage's previous tile has been read) and has
-        // landed by the next barrier.  Same barrier count as the compute
-        // waves; the stage-0 query staging of the fused prologue is finished
-        // before the first barrier.
-        if (ntiles > 0) issue_tile(0);
-        for (int it = 0; it < ntiles; ++it) {
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (it + 1 < ntiles) issue_tile(it + 1);
-        }
-        // item end: both stages are free once every wave has passed it, so the
-        // next item's first tile goes out during the compute waves' epilogue
-        __syncthreads();
-        return;
-    } else {
 
     // ------------------------------------------------ Q^T operand (registers)
     // B operand of S^T = K Q^T: lane holds query row (lane & 15), dims 32 s + 8 g4 + j.
@@ -319,7 +355,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         // before any arithmetic.  The rows are staged in LDS (stage 0), where
         // the RoPE partner dims are read back and the operand is read
         // transposed.
-        uint16_t* qs = reinterpret_cast<uint16_t*>(lds) + wave * 16 * D;
+        uint16_t* qs = reinterpret_cast<uint16_t*>(lds + (gt & 1) * T::STAGE) + wave * 16 * D;
         constexpr int LPR = D / 8;              // lanes per row, 16 B each
         constexpr int RPI = 64 / LPR;           // rows per instruction
         constexpr int NIN = 16 / RPI;           // instructions per wave
@@ -423,7 +459,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const int vrd1 = T::KBYTES + 16 * (8 * (lane & 15) + ((4 + g4) ^ vx));
     for (int it = 0; it < ntiles; ++it) {
         const int k0 = it * 64;
-        const int st = (it + 1) & 1;
+        const int st = (gt + it + 1) & 1;
         __syncthreads();                // the copy waves' tile `it` has landed; stage st^1 is free again
         if (k0 >= lim_wave) continue;   // the whole tile is past this wave's rows
 
@@ -531,8 +567,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     // O^T C layout: lane holds row myrow, dims 16 d + 4 g4 + i.
     const float l_tot = lacc[0];
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    if (!row_ok) return;
     if constexpr (!FUSED) {
+        if (!row_ok) return;
         float* orow = p.out_f32 + b * p.o_bs + h * p.o_hs + static_cast<int64_t>(myrow) * p.o_rs;
 #pragma unroll
         for (int d = 0; d < DBK; ++d) {
@@ -541,51 +577,68 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         }
     } else {
         // bf16(attn) * sigmoid(gate), bf16 out [S, Hq*D] (prefill_engine.rs:2263-2308).
-        uint16_t* orow = p.out_bf16 + static_cast<int64_t>(myrow) * p.Hq * D + h * D;
-        const uint16_t* grow = p.gate + h * p.q_hs + static_cast<int64_t>(myrow) * p.q_rs;
-        // all gate loads first (the output stores could alias them as far as
-        // the compiler knows, which would serialise one load per store)
-        u32x2_v gwa[DBK];
+        // The accumulator layout gives a lane 8 bytes of each of 16 rows, so
+        // the rows go through the wave's own LDS rows (the stage the next
+        // item stages its queries in; its tiles are read by now) and the gate
+        // loads and output stores move 16 contiguous bytes a lane: row
+        // k RPI + rr, dims 8c .. 8c+7.  16-byte chunks are XOR-swizzled by
+        // row, so the 16 rows of a write land in different banks.
+        constexpr int LPR = D / 8, RPI = 64 / LPR, NIN = 16 / RPI, CM = LPR - 1;
+        // the lane index afresh (mbcnt), so that no new value stays live
+        // through the key loop, which runs at the register limit
+        const int ln = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+        const int c = ln % LPR, rr = ln / LPR, g4e = ln >> 4;
+        u32x4_v gq[NIN];
 #pragma unroll
-        for (int d = 0; d < DBK; ++d) gwa[d] = *reinterpret_cast<const u32x2_v*>(grow + 16 * d + 4 * g4);
+        for (int k = 0; k < NIN; ++k) {
+            const int row = min(row_w0 + k * RPI + rr, S - 1);
+            gq[k] = ld16(p.gate + h * p.q_hs + static_cast<int64_t>(row) * p.q_rs + 8 * c);
+        }
+        uint8_t* const os = lds + ((gt + ntiles) & 1) * T::STAGE + wave * 16 * D * 2;
+        const int r16 = ln & 15;
 #pragma unroll
         for (int d = 0; d < DBK; ++d) {
-            const int dd = 16 * d + 4 * g4;
-            const u32x2_v gw = gwa[d];
-            const float gv[4] = {bf16_bits_to_f32(gw[0] & 0xFFFFu), bf16_bits_to_f32(gw[0] >> 16),
-                                 bf16_bits_to_f32(gw[1] & 0xFFFFu), bf16_bits_to_f32(gw[1] >> 16)};
-            float r[4];
+            const int ch = 2 * d + (g4e >> 1);
+            const u32x2_v a = {cvt_pk<bf16_t>(oacc[d][0] * inv, oacc[d][1] * inv),
+                               cvt_pk<bf16_t>(oacc[d][2] * inv, oacc[d][3] * inv)};
+            *reinterpret_cast<u32x2_v*>(os + r16 * D * 2 + ((ch ^ (r16 & CM)) * 16) + (g4e & 1) * 8) = a;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) {
+            const int rl = k * RPI + rr, row = row_w0 + rl;
+            const u32x4_v av = ld16(os + rl * D * 2 + ((c ^ (rl & CM)) * 16));
+            u32x4_v o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t ab = cvt_pk<bf16_t>(oacc[d][e] * inv, 0.f);
-                const float a = bf16_bits_to_f32(ab & 0xFFFFu);
-                // sigmoid(g) = 1 / (1 + 2^(-g log2 e)), hardware exp2 and reciprocal
-                r[e] = a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv[e] * kLog2e));
+                float r2[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const float a = bf16_bits_to_f32(hh ? av[e] >> 16 : av[e] & 0xFFFFu);
+                    const float g = bf16_bits_to_f32(hh ? gq[k][e] >> 16 : gq[k][e] & 0xFFFFu);
+                    // sigmoid(g) = 1 / (1 + 2^(-g log2 e)), hardware exp2 and reciprocal
+                    r2[hh] = a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
+                }
+                o[e] = cvt_pk<bf16_t>(r2[0], r2[1]);
             }
-            const u32x2_v o = {cvt_pk<bf16_t>(r[0], r[1]), cvt_pk<bf16_t>(r[2], r[3])};
-            *reinterpret_cast<u32x2_v*>(orow + dd) = o;
+            if (row < S) st16(p.out_bf16 + static_cast<int64_t>(row) * p.Hq * D + h * D + 8 * c, o);
         }
     }
-    }  // compute waves
     };
 
     // Separate loops for the copy and the compute waves (same items, same
     // barrier count per item), so neither keeps the other's registers live.
-    // The next item is read after the item-end barrier of the current one.
-    auto for_items = [&](auto copy_tag) {
-        for (int r = 0;; ++r) {
-            const int m = (r & 1) ? (r + 1) * W - 1 - j : r * W + j;
-            if (m >= n_items) break;          // the sequence of m is increasing
-            const int qt = p.nqt - 1 - m / (hpi * p.B);
-            const int rem = m % (hpi * p.B);
-            const int h = (by_xcd ? (bid & 7) * hpx : 0) + rem % hpi;
-            run_item(copy_tag, qt, h, rem / hpi);
+    if (wave >= kPrefillWaves) {
+        copy_items();
+    } else {
+        int gt = 0, qt, h, b;
+        for (int r = 0; item_at(r, qt, h, b); ++r) {
+            run_item(qt, h, b, gt);
+            gt += tiles_of(qt);
         }
-    };
-    if (wave >= kPrefillWaves)
-        for_items(std::true_type{});
-    else
-        for_items(std::false_type{});
+    }
 #endif
 }
 

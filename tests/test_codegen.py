@@ -79,3 +79,54 @@ def test_loop_scratch_parser():
     found = loop_scratch(asm)
     assert list(found) == ["_ZN3ssa19decode_split_kernelIXEEvv"]
     assert found["_ZN3ssa19decode_split_kernelIXEEvv"] == ["scratch_load_dword v2, off, off"]
+
+
+PREFILL = re.compile(r"^(_ZN3ssa14prefill_kernel[^:\s]*Li256[^:\s]*):")
+
+
+def key_loop_read_ahead(lines):
+    """{prefill kernel: K operand reads issued back to back ahead of the QK^T
+    MFMAs}.  The source asks for kKLA (8) of them with a scheduling group whose
+    marker the assembly listing keeps ("sched_group_barrier mask(0x00000100)
+    size(8) SyncID(0)"); this counts the ds_read_b128 run that ends at the
+    marker.  The compiler keeps the run only while it has the registers."""
+    found, name, run = {}, None, 0
+    for ln in lines:
+        m = PREFILL.match(ln)
+        if m:
+            name, run = m.group(1), 0
+            continue
+        if name is None or name in found:
+            continue
+        ins = ln.strip()
+        if "sched_group_barrier mask(0x00000100) size(8) SyncID(0)" in ins:
+            found[name] = run
+        elif ins.startswith("ds_read_b128"):
+            run += 1
+        elif ins and not ins.startswith(";"):
+            run = 0
+    return found
+
+
+def test_key_loop_read_ahead_parser():
+    """The parser on hand-written listings: eight reads ahead pass, a read
+    interleaved with its MFMA is found."""
+    head = "_ZN3ssa14prefill_kernelIXLi256EEvv:\n"
+    marker = "\t; sched_group_barrier mask(0x00000100) size(8) SyncID(0)\n"
+    good = head + "\ts_mul_i32 s1, s1, 0x10400\n" + "\tds_read_b128 v[0:3], v9\n" * 8 + marker
+    bad = head + "\tds_read_b128 v[0:3], v9\n\ts_waitcnt lgkmcnt(0)\n\tv_mfma_f32_16x16x32_bf16 v[4:7], v[0:3], v[8:11], 0\n" \
+        "\tds_read_b128 v[0:3], v9\n" + marker
+    assert key_loop_read_ahead(good.split("\n")) == {"_ZN3ssa14prefill_kernelIXLi256EEvv": 8}
+    assert key_loop_read_ahead(bad.split("\n")) == {"_ZN3ssa14prefill_kernelIXLi256EEvv": 1}
+
+
+@pytest.mark.slow
+def test_prefill_key_loop_reads_ahead(tmp_path):
+    """The D=256 prefill kernels run at the register limit of three waves a
+    SIMD; a few more values live across the key loop made the compiler issue
+    one K read per MFMA instead of eight ahead (measured: 3060 -> 5350 cycles
+    a key tile).  This checks the look-ahead in the assembly."""
+    found = key_loop_read_ahead(_asm(os.path.join(B.CSRC, "prefill.hip"), str(tmp_path)))
+    assert found, "no D=256 prefill kernels found in the assembly"
+    bad = {k: v for k, v in found.items() if v < 8}
+    assert not bad, f"K reads ahead of the first QK MFMA: {bad}"
