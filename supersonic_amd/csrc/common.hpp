@@ -180,6 +180,16 @@ __device__ __forceinline__ float part_dec(uint32_t w) { return __uint_as_float(~
 __device__ __forceinline__ void store_part(float* p, float v) { store_agent_u32(reinterpret_cast<uint32_t*>(p), part_enc(v)); }
 constexpr int kMergePoll = 1 << 16;
 
+// Words between the split arrival counters of a call with `pairs` (sequence,
+// kv head) pairs in a region of `words` counters: 32 (one 128-byte line each,
+// so the atomics of different pairs do not queue on one line) or, for many
+// pairs, the largest power of two that fits.
+__host__ __device__ constexpr int arrival_stride(long long pairs, long long words) {
+    int s = 32;
+    while (s > 1 && pairs * s > words) s >>= 1;
+    return s;
+}
+
 // Sticky error word of this code object (each translation unit holds its own
 // copy on every GPU): a bounded wait that gives up sets its bit and the kernel
 // carries on to a normal exit.  The host reads and clears it with

@@ -188,6 +188,7 @@ static int run_decode(DecodeRequest& r) {
     p.det = decode_deterministic();
     p.scale_log2 = r.scale * kLog2e;
     p.arrivals = static_cast<unsigned*>(ws);
+    p.arr_stride = arrival_stride(static_cast<long long>(r.B) * r.Hkv, kMaxArrivals);
     p.merge_polls = wait_polls(kMergePoll);
     p.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes);
     p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + kArrivalBytes + align256(rows * r.D * sizeof(float)));

@@ -43,6 +43,7 @@ struct DecodeParams {
     float* part_o;            // [rows, D], row of (b, h, split) = pre_b * Hq + h * n_b + split
     float* part_ml;           // [rows, 2] (max in log2 units, sum)
     unsigned* arrivals;       // [B, Hkv] split arrival counters, zero between calls
+    int arr_stride;           // words between two counters (each on its own cache line when it fits)
     int merge_polls;          // bound of the merge's poll for partials in flight (kMergePoll)
     const uint16_t* gate;     // NULL, or gate element (b, h, d) at b*g_bstride + h*g_hstride + d
     int64_t g_bstride, g_hstride;
@@ -711,7 +712,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // in LDS and merges them all, polling for the others' partials, which are
     // stored or on their way.
     unsigned arrival = 0;
-    if (wave == NW - 1 && lane == 0) arrival = atomicAdd(&p.arrivals[b * p.Hkv + kvh], 1u);
+    if (wave == NW - 1 && lane == 0) arrival = atomicAdd(&p.arrivals[(b * p.Hkv + kvh) * p.arr_stride], 1u);
     float ltot[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
@@ -959,7 +960,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         lds_barrier();
         lds_barrier();
     }
-    if (tid == 0) p.arrivals[b * p.Hkv + kvh] = 0u;  // every split has arrived: ready for the next call
+    if (tid == 0) p.arrivals[(b * p.Hkv + kvh) * p.arr_stride] = 0u;  // every split has arrived: ready for the next call
 }
 
 }  // namespace ssa

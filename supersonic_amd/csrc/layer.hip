@@ -396,6 +396,7 @@ extern "C" int supersonic_attn_gfx950_decode_layer(
     p.part_o = reinterpret_cast<float*>(ws + L.part_o);
     p.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
     p.arrivals = reinterpret_cast<unsigned*>(ws + L.arrivals);
+    p.arr_stride = arrival_stride(static_cast<long long>(B) * Hkv, static_cast<long long>(kLayerArrivalBytes / 4));
     p.gate = q_proj + D;
     p.g_bstride = static_cast<int64_t>(nq);
     p.g_hstride = 2 * static_cast<int64_t>(D);
