@@ -203,6 +203,24 @@ def test_fused_decode_many_ragged_sequences():
         assert torch.equal(cache.v[b, :, lens[b]].cpu(), v_ref[b, :, lens[b]])
 
 
+def test_fused_decode_many_pairs_counter_stride():
+    """640 (sequence, kv head) pairs: the split arrival counters no longer fit one
+    128-byte line each in the counter region and pack at a smaller stride; the
+    result and the counters' reset must not depend on it."""
+    announce("fused decode B=160 Hkv=4 (counter stride 16)")
+    g = gen(43)
+    B, Hq, Hkv, D = 160, 8, 4, 64
+    lens = torch.randint(0, 120, (B,), generator=g).tolist()
+    lens[7], lens[150] = 0, 119
+    case = make_decode_case(23, B, Hq, Hkv, D, 16, lens)
+    ws = torch.zeros(K.decode_workspace_size(B, Hq, Hkv, D, 120), dtype=torch.uint8, device=DEV)
+    for _ in range(2):
+        out, _ = run_fused(case, workspace=ws)
+    ref, _, _, _, _ = oracle_decode(case)
+    check(out, ref, TOL_BF16, "fused B=160 Hkv=4")
+    assert int(ws[:65536].count_nonzero()) == 0, "arrival counters not reset"
+
+
 def test_decode_attend_ragged_with_empty_sequences():
     """decode_attend over ragged kv_lens with empty sequences (zero output) and
     B > 64 (multi-pass device plan)."""
