@@ -24,6 +24,7 @@ typedef float f32x16_v __attribute__((ext_vector_type(16)));
 typedef float f32x2_v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+typedef short s16x4_v __attribute__((ext_vector_type(4)));  // 4 x 16-bit MFMA operand (16x16x16)
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
@@ -124,6 +125,33 @@ __device__ __forceinline__ float row16_sum(float x) {
     x += dpp_f32<0x122>(x);
     x += dpp_f32<0x121>(x);
     return x;
+}
+// Reductions over lanes l ^ 16 and l ^ 32 with the gfx950 permlane swaps
+// (VALU, no LDS round trip).  Each swap returns the lane's own value and its
+// partner's in some order, which is all a max or a sum needs.
+// max of three MFMA results as one v_max3_f32.  fmaxf would first quiet
+// every operand (a v_max_f32 x, x per value) because MFMA outputs are not
+// known to be canonical; scores are never signalling NaNs.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float xor16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return max3_raw(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return max3_raw(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 __device__ __forceinline__ float wave_sum(float x) {
     x = row16_sum(x);

@@ -165,6 +165,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     constexpr int TPI = 64 / LPT;    // tokens per V load instruction
     constexpr int VINS = 16 / TPI;   // V load instructions per 16-token block
     constexpr int ESZ = FP8 ? 1 : 2;
+    constexpr int VQD = D / 16;      // e4m3 V: dims per lane and token (PV on the MFMA pipe)
+    constexpr int VQW = VQD / 4;     // ... in 32-bit words
+    typedef typename U32N<VQW>::t v8_t;
 
     constexpr int NW = decode_waves(GP);
     constexpr int NT = 64 * NW;
@@ -326,7 +329,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         op_t kb[FP8 ? 1 : KSTEPS];
         u32x4_v kr8[FP8 ? KSTEPS / 2 : 1];  // raw e4m3 K, 16 dims a load: converted when the block is processed
         u32x4_v vr16[FP8 ? 1 : VINS];
-        u32x2_v vr8[FP8 ? VINS : 1];
+        v8_t vq[FP8 ? 4 : 1];               // raw e4m3 V: token 4(lane>>4)+j, dims VQD(lane&15) .. +VQD-1
         float ksc, vsc;
     };
     // Buffer resources bound to the block's live rows (a block lies inside one
@@ -338,6 +341,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // MI355X); the FP8 and 4-wave variants measured faster without it.
     constexpr int kStream = (!FP8 && NW == 8) ? 2 : 0;
     const int v_lane_off = (vt * D + vd) * ESZ;
+    const int vq_lane_off = 4 * (lane >> 4) * D + VQD * (lane & 15);  // e4m3 V (bytes)
     auto fetch = [&](int blk, Blk& B) {
         const int t0 = t_begin + blk * 16;
         // The page comes through the scalar cache (lgkmcnt): waiting for it
@@ -359,12 +363,21 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             for (int ss = 0; ss < KSTEPS / 2; ++ss)
                 B.kr8[ss] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * ss, 0, kStream));
         }
-        // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
+        if constexpr (!FP8) {
+            // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
 #pragma unroll
-        for (int j = 0; j < VINS; ++j) {
-            const int jo = TPI * j * D * ESZ;
-            if constexpr (!FP8) B.vr16[j] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane_off, jo, kStream));
-            else B.vr8[j] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane_off, jo, kStream));
+            for (int j = 0; j < VINS; ++j)
+                B.vr16[j] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane_off, TPI * j * D * ESZ, kStream));
+        } else {
+            // V rows in the layout of the PV MFMA's A operand (see process8):
+            // lane owns VQD consecutive dims of tokens 4(lane>>4) .. +3, one
+            // load per token; 16 lanes cover a token's row.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (VQW == 4) B.vq[j] = __builtin_bit_cast(v8_t, __builtin_amdgcn_raw_buffer_load_b128(vr, vq_lane_off, j * D, kStream));
+                else if constexpr (VQW == 2) B.vq[j] = __builtin_bit_cast(v8_t, __builtin_amdgcn_raw_buffer_load_b64(vr, vq_lane_off, j * D, kStream));
+                else B.vq[j] = __builtin_amdgcn_raw_buffer_load_b32(vr, vq_lane_off, j * D, kStream);
+            }
         }
         B.ksc = 1.f;
         B.vsc = 1.f;
@@ -630,14 +643,68 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     };
+    // e4m3 K/V: the scores come out transposed (S^T = K Q^T on the same
+    // operands: lane = head lane&15, tokens 4(lane>>4) + i), which is already
+    // the layout of the probabilities as the B operand of the PV MFMA
+    // (16x16x16: k = tokens 4(lane>>4) .. +3, n = head).  V^T is its A
+    // operand (m = dim, k = token): the lane's four token rows (VQD dims each)
+    // are interleaved by byte permutes ahead of the exact e4m3 -> bf16
+    // converts.  o8[s] holds, for head lane&15, dims VQD(4(lane>>4) + i) + s.
+    // The softmax state (m8, l8) belongs to the lane's head; l8 sums only the
+    // lane's tokens until the end.  The V scale goes on p (per token, along
+    // the contraction), the K scale on the score.
+    constexpr int NS = D / 16;
+    f32x4_v o8[FP8 ? NS : 1];
+#pragma unroll
+    for (int s = 0; s < (FP8 ? NS : 1); ++s) o8[s] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+    float m8 = -1e30f, l8 = 0.f;
+    auto process8 = [&](int nv, const op_t (&kb)[KSTEPS], float ksc, float vsc, auto&& vpairs) {
+        f32x4_v sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) sc = Mfma<QT>::mma(kb[s], as_op<op_t>(qop_s[s * 64 + lane]), sc);
+        // the scales of tokens 4(lane>>4) + i, from the lanes that loaded them
+        const int t4 = 4 * (lane >> 4);
+        float s2[4], ps[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ks = __shfl(ksc, (lane & 48) + t4 + i);
+            s2[i] = t4 + i < nv ? sc[i] * (p.scale_log2 * ks) : -INFINITY;
+        }
+        float bm = max3_raw(s2[0], s2[1], fmaxf(s2[2], s2[3]));
+        bm = xor32_max(xor16_max(bm));
+        const float mn = fmaxf(m8, bm);
+        const float al = __builtin_amdgcn_exp2f(m8 - mn);
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float pe = __builtin_amdgcn_exp2f(s2[i] - mn);
+            sum += pe;
+            ps[i] = pe * __shfl(vsc, (lane & 48) + t4 + i);
+        }
+        l8 = l8 * al + sum;
+        m8 = mn;
+        // rescale only when some head's running max moved (a scalar branch)
+        if (__builtin_amdgcn_ballot_w64(al != 1.0f) != 0) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) o8[s] *= al;
+        }
+        const u32x2_v pw = {pack2<bf16_t>(ps[0], ps[1]), pack2<bf16_t>(ps[2], ps[3])};
+        const s16x4_v pop = __builtin_bit_cast(s16x4_v, pw);
+#pragma unroll
+        for (int w = 0; w < VQW; ++w) {
+            uint32_t vp[4][2];  // bf16 pairs (tokens 2h, 2h+1) of dim 4w + q
+            vpairs(w, vp);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32x2_v a = {vp[q][0], vp[q][1]};
+                o8[4 * w + q] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_v, a), pop, o8[4 * w + q], 0, 0, 0);
+            }
+        }
+    };
     auto process_blk = [&](int blk, Blk& B) {
         const int t0 = t_begin + blk * 16;
-        auto vdec = [&](int j, float (&vf)[8]) {
-            if constexpr (!FP8) unpack8<QT>(B.vr16[j], vf);
-            else fp8x8_to_f32(B.vr8[j], vf);
-        };
         if constexpr (!FP8) {
-            process(min(16, t_main - t0), B.kb, B.ksc, B.vsc, vdec);
+            process(min(16, t_main - t0), B.kb, B.ksc, B.vsc, [&](int j, float (&vf)[8]) { unpack8<QT>(B.vr16[j], vf); });
         } else {
             op_t kb[KSTEPS];
 #pragma unroll
@@ -645,7 +712,27 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                 const u32x4_v& w = B.kr8[s >> 1];
                 kb[s] = as_op<op_t>(fp8x8_to_bf16x8((s & 1) ? u32x2_v{w[2], w[3]} : u32x2_v{w[0], w[1]}));
             }
-            process(min(16, t_main - t0), kb, B.ksc, B.vsc, vdec);
+            // word w of the lane's four token rows -> the bf16 pairs of dims
+            // 4w .. 4w+3: v_perm_b32 takes byte q of tokens 0 and 1 (2 and 3)
+            // side by side, one convert per pair
+            auto vpairs = [&](int w, uint32_t (&vp)[4][2]) {
+                uint32_t r[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (VQW == 1) r[j] = B.vq[j];
+                    else r[j] = B.vq[j][w];
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t lo = __builtin_amdgcn_perm(r[2 * h + 1], r[2 * h], 0x05010400u);  // bytes 0, 1
+                    const uint32_t hi = __builtin_amdgcn_perm(r[2 * h + 1], r[2 * h], 0x07030602u);  // bytes 2, 3
+                    vp[0][h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+                    vp[1][h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+                    vp[2][h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+                    vp[3][h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
+                }
+            };
+            process8(min(16, t_main - t0), kb, B.ksc, B.vsc, vpairs);
         }
     };
 
@@ -698,11 +785,22 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(kn_s[d0 + 2 * j], kn_s[d0 + 2 * j + 1]);
             kbn[s] = as_op<op_t>(w);
         }
-        process(1, kbn, 1.f, 1.f, [&](int j, float (&vf)[8]) {
-            const bool mine = TPI * j + vt == 0;
+        if constexpr (!FP8) {
+            process(1, kbn, 1.f, 1.f, [&](int j, float (&vf)[8]) {
+                const bool mine = TPI * j + vt == 0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vf[e] = mine ? vn_s[vd + e] : 0.f;
-        });
+                for (int e = 0; e < 8; ++e) vf[e] = mine ? vn_s[vd + e] : 0.f;
+            });
+        } else {
+            // token 0 of the block is row 0 of lanes 0..15 (their dims VQD(lane) ..)
+            process8(1, kbn, 1.f, 1.f, [&](int w, uint32_t (&vp)[4][2]) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    vp[q][0] = lane < 16 ? f32_to_bf16_bits(vn_s[VQD * lane + 4 * w + q]) : 0u;
+                    vp[q][1] = 0u;
+                }
+            });
+        }
     }
 
     // ---------------------------------------------------------------- merge
@@ -713,51 +811,80 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // stored or on their way.
     unsigned arrival = 0;
     if (wave == NW - 1 && lane == 0) arrival = atomicAdd(&p.arrivals[(b * p.Hkv + kvh) * p.arr_stride], 1u);
-    float ltot[4];
+    int& last_s = L.last_s;
+    if constexpr (!FP8) {
+        float ltot[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
+        for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
 #pragma unroll
-    for (int off = LPT; off < 64; off <<= 1)
+        for (int off = LPT; off < 64; off <<= 1)
 #pragma unroll
-        for (int h = 0; h < GP; ++h)
+            for (int h = 0; h < GP; ++h)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
+                for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
 
-    if ((lane & 15) == 0) {
+        if ((lane & 15) == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int h = 4 * (lane >> 4) + i;
-            if (h < GP) {
-                ml_s[wave][h][0] = m[i];
-                ml_s[wave][h][1] = ltot[i];
+            for (int i = 0; i < 4; ++i) {
+                const int h = 4 * (lane >> 4) + i;
+                if (h < GP) {
+                    ml_s[wave][h][0] = m[i];
+                    ml_s[wave][h][1] = ltot[i];
+                }
             }
         }
-    }
-    __syncthreads();
-    float fw[GP];
+        __syncthreads();
+        float fw[GP];
 #pragma unroll
-    for (int h = 0; h < GP; ++h) {
-        float M = ml_s[0][h][0];
+        for (int h = 0; h < GP; ++h) {
+            float M = ml_s[0][h][0];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
-        fw[h] = exp2f(ml_s[wave][h][0] - M);
-    }
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
-
-    // One LDS round: every wave parks its scaled sums in its own slot; the
-    // split's partial is then the sum of the NW slots.
-    int& last_s = L.last_s;
-    if (wave == NW - 1 && lane == 0) last_s = arrival == static_cast<unsigned>(ns - 1);
-    if (lane < LPT) {
+            for (int w = 1; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
+            fw[h] = exp2f(ml_s[wave][h][0] - M);
+        }
 #pragma unroll
         for (int h = 0; h < GP; ++h)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) smem[(wave * GP + h) * D + vd + e] = acc[h][e];
+            for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
+
+        // One LDS round: every wave parks its scaled sums in its own slot; the
+        // split's partial is then the sum of the NW slots.
+        if (wave == NW - 1 && lane == 0) last_s = arrival == static_cast<unsigned>(ns - 1);
+        if (lane < LPT) {
+#pragma unroll
+            for (int h = 0; h < GP; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) smem[(wave * GP + h) * D + vd + e] = acc[h][e];
+        }
+        __syncthreads();
+    } else {
+        // the lane's head: running max (the same in the four rows) and sum
+        // over all its tokens; the waves' partials scaled to the common max
+        const float lt = xor32_sum(xor16_sum(l8));
+        const int hl = lane & 15;
+        if (lane < GP) {
+            ml_s[wave][lane][0] = m8;
+            ml_s[wave][lane][1] = lt;
+        }
+        __syncthreads();
+        const int hc = min(hl, GP - 1);
+        float M = ml_s[0][hc][0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) M = fmaxf(M, ml_s[w][hc][0]);
+        const float f = exp2f(ml_s[wave][hc][0] - M);
+        if (wave == NW - 1 && lane == 0) last_s = arrival == static_cast<unsigned>(ns - 1);
+        if (hl < GP) {
+            float* const row = &smem[(wave * GP + hl) * D];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int s4 = 0; s4 < NS / 4; ++s4) {
+                    const f32x4_v v = {o8[4 * s4][i] * f, o8[4 * s4 + 1][i] * f, o8[4 * s4 + 2][i] * f, o8[4 * s4 + 3][i] * f};
+                    *reinterpret_cast<f32x4_v*>(row + VQD * (4 * (lane >> 4) + i) + 4 * s4) = v;
+                }
+        }
+        __syncthreads();
     }
-    __syncthreads();
     // (M, L) of head hh of this split, from the waves' (m, l)
     auto own_ml = [&](int hh, float& M, float& Lsum) {
         M = -1e30f;

@@ -106,34 +106,6 @@ template <> __device__ __forceinline__ uint32_t cvt_pk<f16_t>(float a, float b) 
 template <typename QT> constexpr uint32_t kOnePair = 0x3F803F80u;  // bf16 1.0, 1.0
 template <> constexpr uint32_t kOnePair<f16_t> = 0x3C003C00u;       // f16 1.0, 1.0
 
-// Reductions over lanes l ^ 16 and l ^ 32 with the gfx950 permlane swaps
-// (VALU, no LDS round trip).  Each swap returns the lane's own value and its
-// partner's in some order, which is all a max or a sum needs.
-// max of three MFMA results as one v_max3_f32.  fmaxf would first quiet
-// every operand (a v_max_f32 x, x per value) because MFMA outputs are not
-// known to be canonical; scores are never signalling NaNs.
-__device__ __forceinline__ float max3_raw(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float xor16_max(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return max3_raw(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor32_max(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return max3_raw(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor16_sum(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xor32_sum(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // Tile geometry.  A K tile is 64 keys x D in LDS.  Copy instruction i
 // (i < NR = D/8) of a tile moves rows i, i + NR, i + 2 NR, ... (64/NR rows,
 // one 1 KB run) into LDS block i.  K blocks are padded by 8 words so the
