@@ -56,11 +56,18 @@ template <> struct Mfma<bf16_t> {
     static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
+    static __device__ __forceinline__ f32x4_v mma16(const s16x4_v& a, const s16x4_v& b, const f32x4_v& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
 };
 template <> struct Mfma<f16_t> {
     typedef f16x8_v op;
     static __device__ __forceinline__ f32x4_v mma(const op& a, const op& b, const f32x4_v& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4_v mma16(const s16x4_v& a, const s16x4_v& b, const f32x4_v& c) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
     }
 };
 
@@ -93,18 +100,6 @@ __device__ __forceinline__ constexpr int kdim(int s, int g) {
     return FP8 ? 64 * (s >> 1) + 16 * g + 8 * (s & 1) : 32 * s + 8 * g;
 }
 
-__device__ __forceinline__ void fp8x8_to_f32(u32x2_v w, float* f) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        f32x2_v lo = fp8x2_to_f32(w[i], false);
-        f32x2_v hi = fp8x2_to_f32(w[i], true);
-        f[4 * i + 0] = lo[0];
-        f[4 * i + 1] = lo[1];
-        f[4 * i + 2] = hi[0];
-        f[4 * i + 3] = hi[1];
-    }
-}
-
 // Buffer resource for a base that is uniform across the wave (forced into
 // SGPRs: it can come from a block-table load the compiler cannot prove
 // uniform).  Reads at or past `bytes` return zeros.
@@ -132,7 +127,6 @@ template <int D, int GP>
 struct DecodeLds {
     static constexpr int NW = decode_waves(GP);
     float smem[NW * GP * D];        // q staging, then the wave merge
-    float p_s[NW][16][16];          // per-wave probabilities (heads past GP: padding that every lane may write)
     float kn_s[D], vn_s[D];         // the new token (fused owner split)
     float ml_s[NW][GP][2];
     u32x4_v qop_s[(D / 32) * 64];   // Q as the MFMA A operand
@@ -161,18 +155,18 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     static_assert(decode_waves(GP) * GP >= 16, "smem holds the 16 padded Q rows");
     typedef typename Mfma<QT>::op op_t;
     constexpr int KSTEPS = D / 32;
-    constexpr int LPT = D / 8;       // lanes per token row in the V layout
-    constexpr int TPI = 64 / LPT;    // tokens per V load instruction
-    constexpr int VINS = 16 / TPI;   // V load instructions per 16-token block
     constexpr int ESZ = FP8 ? 1 : 2;
-    constexpr int VQD = D / 16;      // e4m3 V: dims per lane and token (PV on the MFMA pipe)
-    constexpr int VQW = VQD / 4;     // ... in 32-bit words
-    typedef typename U32N<VQW>::t v8_t;
+    constexpr int VQD = D / 16;      // V dims per lane and token (PV A operand)
+    constexpr int VQW = VQD * ESZ / 4;  // ... in 32-bit words
+    constexpr int VCE = 16 / ESZ;       // elements of a 16-byte chunk
+    auto vdim = [](int w, int q, int m) {
+        if constexpr (VQW >= 4) return (w / (VCE / 4)) * 16 * VCE + VCE * m + 4 * (w % (VCE / 4)) + q;
+        else return VQD * m + 4 * w + q;
+    };
 
     constexpr int NW = decode_waves(GP);
     constexpr int NT = 64 * NW;
     float (&smem)[NW * GP * D] = L.smem;
-    float (&p_s)[NW][16][16] = L.p_s;
     float (&kn_s)[D] = L.kn_s;
     float (&vn_s)[D] = L.vn_s;
     float (&ml_s)[NW][GP][2] = L.ml_s;
@@ -315,8 +309,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     }
 
     const int n_s = lane & 15;           // score lane: token within the block
-    const int vt = lane / LPT;           // V lane: token within the instruction
-    const int vd = (lane % LPT) * 8;     // V lane: first dim
     // Cached tokens of this split; the owner's new token (the last one) is
     // handled after the loop.
     const int t_main = owner ? pos : t_end;
@@ -328,8 +320,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     struct Blk {
         op_t kb[FP8 ? 1 : KSTEPS];
         u32x4_v kr8[FP8 ? KSTEPS / 2 : 1];  // raw e4m3 K, 16 dims a load: converted when the block is processed
-        u32x4_v vr16[FP8 ? 1 : VINS];
-        v8_t vq[FP8 ? 4 : 1];               // raw e4m3 V: token 4(lane>>4)+j, dims VQD(lane&15) .. +VQD-1
+        uint32_t vq[4][VQW];                // V of token 4(lane>>4)+j, the dims vdim(., ., lane&15)
         float ksc, vsc;
     };
     // Buffer resources bound to the block's live rows (a block lies inside one
@@ -340,8 +331,11 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // (every byte is read once; 6.0 -> 7.1 TB/s for its access pattern on
     // MI355X); the FP8 and 4-wave variants measured faster without it.
     constexpr int kStream = (!FP8 && NW == 8) ? 2 : 0;
-    const int v_lane_off = (vt * D + vd) * ESZ;
-    const int vq_lane_off = 4 * (lane >> 4) * D + VQD * (lane & 15);  // e4m3 V (bytes)
+    // V as the PV MFMA's A operand: a lane's V bytes of a token are 16-byte chunks, chunk c
+    // at 16 (lane & 15) + 256 c, so each load instruction reads 256
+    // consecutive bytes of the row across 16 lanes; vdim maps (4-dim group w,
+    // q, row m) of the A operand to the dim the lane holds there.
+    const int vq_lane_off = 4 * (lane >> 4) * D * ESZ + (VQW >= 4 ? 16 : VQD * ESZ) * (lane & 15);
     auto fetch = [&](int blk, Blk& B) {
         const int t0 = t_begin + blk * 16;
         // The page comes through the scalar cache (lgkmcnt): waiting for it
@@ -352,7 +346,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         const int nvalid = __builtin_amdgcn_readfirstlane(max(0, min(16, t_main - t0)));  // wave-uniform
         const __amdgpu_buffer_rsrc_t kr = uniform_rsrc(kbase + base * ESZ, nvalid * D * ESZ);
         const __amdgpu_buffer_rsrc_t vr = uniform_rsrc(vbase + base * ESZ, nvalid * D * ESZ);
-        // K as the MFMA B operand: col = token n_s, k = dims 32s + 8(lane>>4) + j.
+        // K as the QK^T MFMA's A operand: row = token n_s, k = dims kdim(s, lane>>4) + j.
         if constexpr (!FP8) {
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s)
@@ -363,20 +357,25 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             for (int ss = 0; ss < KSTEPS / 2; ++ss)
                 B.kr8[ss] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane_off + 64 * ss, 0, kStream));
         }
-        if constexpr (!FP8) {
-            // V rows: lane owns dims vd..vd+7 of token TPI*j + vt.
-#pragma unroll
-            for (int j = 0; j < VINS; ++j)
-                B.vr16[j] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane_off, TPI * j * D * ESZ, kStream));
-        } else {
-            // V rows in the layout of the PV MFMA's A operand (see process8):
-            // lane owns VQD consecutive dims of tokens 4(lane>>4) .. +3, one
-            // load per token; 16 lanes cover a token's row.
+        {
+            // the lane's four token rows 4(lane>>4) .. +3, VQD dims each;
+            // 16 lanes cover a row
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if constexpr (VQW == 4) B.vq[j] = __builtin_bit_cast(v8_t, __builtin_amdgcn_raw_buffer_load_b128(vr, vq_lane_off, j * D, kStream));
-                else if constexpr (VQW == 2) B.vq[j] = __builtin_bit_cast(v8_t, __builtin_amdgcn_raw_buffer_load_b64(vr, vq_lane_off, j * D, kStream));
-                else B.vq[j] = __builtin_amdgcn_raw_buffer_load_b32(vr, vq_lane_off, j * D, kStream);
+                if constexpr (VQW >= 4) {
+#pragma unroll
+                    for (int c = 0; c < VQW / 4; ++c) {
+                        const u32x4_v w = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(vr, vq_lane_off + 256 * c, j * D * ESZ, kStream));
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) B.vq[j][4 * c + e] = w[e];
+                    }
+                } else if constexpr (VQW == 2) {
+                    const u32x2_v w = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(vr, vq_lane_off, j * D * ESZ, kStream));
+                    B.vq[j][0] = w[0];
+                    B.vq[j][1] = w[1];
+                } else {
+                    B.vq[j][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, vq_lane_off, j * D * ESZ, kStream);
+                }
             }
         }
         B.ksc = 1.f;
@@ -564,101 +563,23 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     lds_barrier();  // smem is reused by the merge below
 
     // ---------------------------------------------------------------- main loop
-    float m[4], lsum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m[i] = -1e30f; lsum[i] = 0.f; }
-    float acc[GP][8];
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-
-    // One 16-token block: scores on the MFMA pipe, online softmax per head,
-    // PV on VALU.  Tokens n_s >= nv are masked.  vdec(j, vf) yields the 8
-    // dims of V row TPI*j + vt as floats.
-    auto process = [&](int nv, const op_t (&kb)[KSTEPS], float ksc, float vsc, auto&& vdec) {
-        f32x4_v sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) sc = Mfma<QT>::mma(as_op<op_t>(qop_s[s * 64 + lane]), kb[s], sc);
-
-        const bool valid = n_s < nv;
-        float pr[4], al[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float s2 = valid ? sc[i] * (p.scale_log2 * ksc) : -INFINITY;
-            const float bm = row16_max(s2);
-            const float mn = fmaxf(m[i], bm);
-            al[i] = __builtin_amdgcn_exp2f(m[i] - mn);
-            const float pe = __builtin_amdgcn_exp2f(s2 - mn);
-            lsum[i] = lsum[i] * al[i] + pe;
-            m[i] = mn;
-            pr[i] = pe * vsc;
-        }
-        {  // every lane: those of heads past GP write the padding (with an
-           // exec-masked store here the layer kernel reloaded a spilled
-           // register inside its main loop, a wait for every load in flight)
-            f32x4_v pv = {pr[0], pr[1], pr[2], pr[3]};
-            *reinterpret_cast<f32x4_v*>(&p_s[wave][n_s][4 * (lane >> 4)]) = pv;
-        }
-        float alpha[GP];
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-            alpha[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[h & 3]), 16 * (h >> 2)));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // Rescale only when some head's running max moved (alpha != 1; the
-        // factors are wave-uniform, so this is a scalar branch): after the
-        // first blocks the max rarely changes.
-        bool moved = false;
-#pragma unroll
-        for (int h = 0; h < GP; ++h) moved |= alpha[h] != 1.0f;
-        if (moved) {
-#pragma unroll
-            for (int h = 0; h < GP; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
-        }
-
-#pragma unroll
-        for (int j = 0; j < VINS; ++j) {
-            const int tn = TPI * j + vt;
-            float vf[8];
-            vdec(j, vf);
-            float pv[GP];
-#pragma unroll
-            for (int h4 = 0; h4 < GP / 4; ++h4) {
-                const f32x4_v t = *reinterpret_cast<const f32x4_v*>(&p_s[wave][tn][4 * h4]);
-                pv[4 * h4] = t[0];
-                pv[4 * h4 + 1] = t[1];
-                pv[4 * h4 + 2] = t[2];
-                pv[4 * h4 + 3] = t[3];
-            }
-#pragma unroll
-            for (int h = 0; h < GP; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pv[h], vf[e], acc[h][e]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-    };
-    // e4m3 K/V: the scores come out transposed (S^T = K Q^T on the same
-    // operands: lane = head lane&15, tokens 4(lane>>4) + i), which is already
-    // the layout of the probabilities as the B operand of the PV MFMA
-    // (16x16x16: k = tokens 4(lane>>4) .. +3, n = head).  V^T is its A
-    // operand (m = dim, k = token): the lane's four token rows (VQD dims each)
-    // are interleaved by byte permutes ahead of the exact e4m3 -> bf16
-    // converts.  o8[s] holds, for head lane&15, dims VQD(4(lane>>4) + i) + s.
-    // The softmax state (m8, l8) belongs to the lane's head; l8 sums only the
-    // lane's tokens until the end.  The V scale goes on p (per token, along
-    // the contraction), the K scale on the score.
+    // One 16-token block, both products on the MFMA pipe.  The scores come
+    // out transposed (S^T = K Q^T: lane = head lane&15, tokens 4(lane>>4) + i),
+    // which is already the layout of the probabilities as the B operand of
+    // the PV MFMA (16x16x16: k = tokens 4(lane>>4) .. +3, n = head).  V^T is
+    // its A operand (m = dim, k = token): the lane's four token rows are
+    // interleaved by byte permutes (vpairs; e4m3 then takes an exact convert
+    // to bf16).  acc[4w + q] holds, for head lane&15, the dims
+    // vdim(w, q, 4(lane>>4) + i).  The softmax state (m_run, l_run) belongs to
+    // the lane's head; l_run sums only the lane's tokens until the end.  FP8:
+    // the V scale goes on p (per token, along the contraction), the K scale
+    // on the score.  Tokens >= nv are masked.
     constexpr int NS = D / 16;
-    f32x4_v o8[FP8 ? NS : 1];
+    f32x4_v acc[NS];
 #pragma unroll
-    for (int s = 0; s < (FP8 ? NS : 1); ++s) o8[s] = f32x4_v{0.f, 0.f, 0.f, 0.f};
-    float m8 = -1e30f, l8 = 0.f;
-    auto process8 = [&](int nv, const op_t (&kb)[KSTEPS], float ksc, float vsc, auto&& vpairs) {
+    for (int s = 0; s < NS; ++s) acc[s] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+    float m_run = -1e30f, l_run = 0.f;
+    auto process = [&](int nv, const op_t (&kb)[KSTEPS], float ksc, float vsc, auto&& vpairs) {
         f32x4_v sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) sc = Mfma<QT>::mma(kb[s], as_op<op_t>(qop_s[s * 64 + lane]), sc);
@@ -667,44 +588,55 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
         float s2[4], ps[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float ks = __shfl(ksc, (lane & 48) + t4 + i);
+            const float ks = FP8 ? __shfl(ksc, (lane & 48) + t4 + i) : 1.f;
             s2[i] = t4 + i < nv ? sc[i] * (p.scale_log2 * ks) : -INFINITY;
         }
         float bm = max3_raw(s2[0], s2[1], fmaxf(s2[2], s2[3]));
         bm = xor32_max(xor16_max(bm));
-        const float mn = fmaxf(m8, bm);
-        const float al = __builtin_amdgcn_exp2f(m8 - mn);
+        const float mn = fmaxf(m_run, bm);
+        const float al = __builtin_amdgcn_exp2f(m_run - mn);
         float sum = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float pe = __builtin_amdgcn_exp2f(s2[i] - mn);
             sum += pe;
-            ps[i] = pe * __shfl(vsc, (lane & 48) + t4 + i);
+            ps[i] = FP8 ? pe * __shfl(vsc, (lane & 48) + t4 + i) : pe;
         }
-        l8 = l8 * al + sum;
-        m8 = mn;
+        l_run = l_run * al + sum;
+        m_run = mn;
         // rescale only when some head's running max moved (a scalar branch)
         if (__builtin_amdgcn_ballot_w64(al != 1.0f) != 0) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s) o8[s] *= al;
+            for (int s = 0; s < NS; ++s) acc[s] *= al;
         }
-        const u32x2_v pw = {pack2<bf16_t>(ps[0], ps[1]), pack2<bf16_t>(ps[2], ps[3])};
+        const u32x2_v pw = {pack2<QT>(ps[0], ps[1]), pack2<QT>(ps[2], ps[3])};
         const s16x4_v pop = __builtin_bit_cast(s16x4_v, pw);
 #pragma unroll
-        for (int w = 0; w < VQW; ++w) {
+        for (int w = 0; w < VQD / 4; ++w) {
             uint32_t vp[4][2];  // bf16 pairs (tokens 2h, 2h+1) of dim 4w + q
             vpairs(w, vp);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const u32x2_v a = {vp[q][0], vp[q][1]};
-                o8[4 * w + q] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_v, a), pop, o8[4 * w + q], 0, 0, 0);
+                acc[4 * w + q] = Mfma<QT>::mma16(__builtin_bit_cast(s16x4_v, a), pop, acc[4 * w + q]);
             }
         }
     };
     auto process_blk = [&](int blk, Blk& B) {
         const int t0 = t_begin + blk * 16;
         if constexpr (!FP8) {
-            process(min(16, t_main - t0), B.kb, B.ksc, B.vsc, [&](int j, float (&vf)[8]) { unpack8<QT>(B.vr16[j], vf); });
+            // words 2w, 2w+1 of the lane's four token rows (dims 4w .. 4w+3)
+            // -> the pairs (tokens 2h, 2h+1) of each dim: one v_perm_b32 each
+            process(min(16, t_main - t0), B.kb, 1.f, 1.f, [&](int w, uint32_t (&vp)[4][2]) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const uint32_t a0 = B.vq[2 * h][2 * w + c], a1 = B.vq[2 * h + 1][2 * w + c];
+                        vp[2 * c][h] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+                        vp[2 * c + 1][h] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
+                    }
+            });
         } else {
             op_t kb[KSTEPS];
 #pragma unroll
@@ -718,10 +650,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             auto vpairs = [&](int w, uint32_t (&vp)[4][2]) {
                 uint32_t r[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if constexpr (VQW == 1) r[j] = B.vq[j];
-                    else r[j] = B.vq[j][w];
-                }
+                for (int j = 0; j < 4; ++j) r[j] = B.vq[j][w];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const uint32_t lo = __builtin_amdgcn_perm(r[2 * h + 1], r[2 * h], 0x05010400u);  // bytes 0, 1
@@ -732,7 +661,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
                     vp[3][h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
                 }
             };
-            process8(min(16, t_main - t0), kb, B.ksc, B.vsc, vpairs);
+            process(min(16, t_main - t0), kb, B.ksc, B.vsc, vpairs);
         }
     };
 
@@ -785,22 +714,14 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
             for (int j = 0; j < 4; ++j) w[j] = pack2<QT>(kn_s[d0 + 2 * j], kn_s[d0 + 2 * j + 1]);
             kbn[s] = as_op<op_t>(w);
         }
-        if constexpr (!FP8) {
-            process(1, kbn, 1.f, 1.f, [&](int j, float (&vf)[8]) {
-                const bool mine = TPI * j + vt == 0;
+        // token 0 of the block is k = 0 of lanes 0..15
+        process(1, kbn, 1.f, 1.f, [&](int w, uint32_t (&vp)[4][2]) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vf[e] = mine ? vn_s[vd + e] : 0.f;
-            });
-        } else {
-            // token 0 of the block is row 0 of lanes 0..15 (their dims VQD(lane) ..)
-            process8(1, kbn, 1.f, 1.f, [&](int w, uint32_t (&vp)[4][2]) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    vp[q][0] = lane < 16 ? f32_to_bf16_bits(vn_s[VQD * lane + 4 * w + q]) : 0u;
-                    vp[q][1] = 0u;
-                }
-            });
-        }
+            for (int q = 0; q < 4; ++q) {
+                vp[q][0] = lane < 16 ? Elem<QT>::from_f32(vn_s[vdim(w, q, lane)]) : 0u;
+                vp[q][1] = 0u;
+            }
+        });
     }
 
     // ---------------------------------------------------------------- merge
@@ -811,80 +732,35 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // stored or on their way.
     unsigned arrival = 0;
     if (wave == NW - 1 && lane == 0) arrival = atomicAdd(&p.arrivals[(b * p.Hkv + kvh) * p.arr_stride], 1u);
+    // One LDS round: the lane's head has its running max (the same in the
+    // four rows) and its sum over all its tokens; every wave parks its sums,
+    // scaled to the workgroup's max, in its own slot, and the split's partial
+    // is then the sum of the NW slots.
     int& last_s = L.last_s;
-    if constexpr (!FP8) {
-        float ltot[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ltot[i] = row16_sum(lsum[i]);
-#pragma unroll
-        for (int off = LPT; off < 64; off <<= 1)
-#pragma unroll
-            for (int h = 0; h < GP; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
-
-        if ((lane & 15) == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int h = 4 * (lane >> 4) + i;
-                if (h < GP) {
-                    ml_s[wave][h][0] = m[i];
-                    ml_s[wave][h][1] = ltot[i];
-                }
-            }
-        }
-        __syncthreads();
-        float fw[GP];
-#pragma unroll
-        for (int h = 0; h < GP; ++h) {
-            float M = ml_s[0][h][0];
-#pragma unroll
-            for (int w = 1; w < NW; ++w) M = fmaxf(M, ml_s[w][h][0]);
-            fw[h] = exp2f(ml_s[wave][h][0] - M);
-        }
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] *= fw[h];
-
-        // One LDS round: every wave parks its scaled sums in its own slot; the
-        // split's partial is then the sum of the NW slots.
-        if (wave == NW - 1 && lane == 0) last_s = arrival == static_cast<unsigned>(ns - 1);
-        if (lane < LPT) {
-#pragma unroll
-            for (int h = 0; h < GP; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) smem[(wave * GP + h) * D + vd + e] = acc[h][e];
-        }
-        __syncthreads();
-    } else {
-        // the lane's head: running max (the same in the four rows) and sum
-        // over all its tokens; the waves' partials scaled to the common max
-        const float lt = xor32_sum(xor16_sum(l8));
-        const int hl = lane & 15;
-        if (lane < GP) {
-            ml_s[wave][lane][0] = m8;
-            ml_s[wave][lane][1] = lt;
-        }
-        __syncthreads();
-        const int hc = min(hl, GP - 1);
-        float M = ml_s[0][hc][0];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) M = fmaxf(M, ml_s[w][hc][0]);
-        const float f = exp2f(ml_s[wave][hc][0] - M);
-        if (wave == NW - 1 && lane == 0) last_s = arrival == static_cast<unsigned>(ns - 1);
-        if (hl < GP) {
-            float* const row = &smem[(wave * GP + hl) * D];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int s4 = 0; s4 < NS / 4; ++s4) {
-                    const f32x4_v v = {o8[4 * s4][i] * f, o8[4 * s4 + 1][i] * f, o8[4 * s4 + 2][i] * f, o8[4 * s4 + 3][i] * f};
-                    *reinterpret_cast<f32x4_v*>(row + VQD * (4 * (lane >> 4) + i) + 4 * s4) = v;
-                }
-        }
-        __syncthreads();
+    const float lt = xor32_sum(xor16_sum(l_run));
+    const int hl = lane & 15;
+    if (lane < GP) {
+        ml_s[wave][lane][0] = m_run;
+        ml_s[wave][lane][1] = lt;
     }
+    __syncthreads();
+    const int hc = min(hl, GP - 1);
+    float mw = ml_s[0][hc][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mw = fmaxf(mw, ml_s[w][hc][0]);
+    const float f = exp2f(ml_s[wave][hc][0] - mw);
+    if (wave == NW - 1 && lane == 0) last_s = arrival == static_cast<unsigned>(ns - 1);
+    if (hl < GP) {
+        float* const row = &smem[(wave * GP + hl) * D];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int s4 = 0; s4 < NS / 4; ++s4) {
+                const f32x4_v v = {acc[4 * s4][i] * f, acc[4 * s4 + 1][i] * f, acc[4 * s4 + 2][i] * f, acc[4 * s4 + 3][i] * f};
+                *reinterpret_cast<f32x4_v*>(row + vdim(s4, 0, 4 * (lane >> 4) + i)) = v;
+            }
+    }
+    __syncthreads();
     // (M, L) of head hh of this split, from the waves' (m, l)
     auto own_ml = [&](int hh, float& M, float& Lsum) {
         M = -1e30f;

@@ -79,7 +79,7 @@ def assert_close_ulps(out, ref, name, floor=0.0):
     ulp = torch.exp2(torch.floor(torch.log2(y.abs().clamp_min(2.0 ** -100))) - 7)
     bad = (x - y).abs() > 2 * ulp + floor
     assert not bad.any(), f"{name}: {int(bad.sum())} entries beyond 2 ulps, max diff {(x - y).abs().max().item():.3e}"
-    assert (x == y).float().mean().item() > 0.9, f"{name}: too few identical entries"
+    assert (x == y).float().mean().item() > 0.75, f"{name}: too few identical entries"
 
 
 def test_decode_eager_runs_agree_to_ulps():
