@@ -3,9 +3,10 @@ output projection + residual) and a fused prefill chunk captured into a HIP
 graph through torch.cuda.CUDAGraph.  The entry points allocate nothing once
 their workspaces exist and record no memset nodes.  The prefill is
 deterministic, so its replays equal the eager result bit for bit; the decode
-waves claim 16-token blocks dynamically, so the fp32 order of their merge (and
-an occasional bf16 rounding) varies between any two runs, eager or replayed:
-its replays are held to two bf16 ulps of the eager result plus an absolute
+waves claim 16-token blocks dynamically, so the fp32 order of their merge and
+the running max against which each probability is rounded to bf16 (the PV
+operand) vary between any two runs, eager or replayed: its replays are held to
+two bf16 ulps of the eager result (and most entries identical) plus an absolute
 2^-8 (entries near zero come from cancellation, and their own ulp is far
 below the summation-order error of the terms).  Replays are
 separated by eager work (the hidden state is reset, outputs are read back)."""
