@@ -327,10 +327,12 @@ __device__ __forceinline__ void decode_split_body(const DecodeParams& p, int vbx
     // page): rows past kv_len read as zeros, so every load is one per-lane
     // offset plus a constant, with no per-load clamping.
     const int k_lane_off = n_s * D * ESZ + kdim<FP8>(0, lane >> 4) * ESZ;
-    // Cache policy of the K/V loads: nontemporal for the bf16 8-wave kernel
-    // (every byte is read once; 6.0 -> 7.1 TB/s for its access pattern on
-    // MI355X); the FP8 and 4-wave variants measured faster without it.
-    constexpr int kStream = (!FP8 && NW == 8) ? 2 : 0;
+    // Cache policy of the K/V loads: nontemporal for 16-bit caches (every
+    // byte is read once; 6.0 -> 7.1 TB/s for the 8-wave kernel's access
+    // pattern on MI355X; the 4-wave kernels measured the same either way);
+    // the e4m3 kernel measured faster without it (59.5 against 63 us at
+    // config 4).
+    constexpr int kStream = FP8 ? 0 : 2;
     // V as the PV MFMA's A operand: a lane's V bytes of a token are 16-byte chunks, chunk c
     // at 16 (lane & 15) + 256 c, so each load instruction reads 256
     // consecutive bytes of the row across 16 lanes; vdim maps (4-dim group w,
