@@ -277,6 +277,23 @@ def test_fused_decode_fp8(B, lens):
         assert torch.allclose(cache.v_scale[b, :, p].cpu(), vs_ref[b, :, p])
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,D,rot,lens", [
+    (2, 8, 1, 128, 32, [300, 17]),     # 8-head group (4-wave kernel), 8-byte V chunks
+    (1, 16, 1, 64, 16, [1000]),        # 16-head group, 4-byte V chunks
+    (3, 4, 2, 64, 16, [5, 64, 130]),   # 2-head group, partial blocks
+])
+def test_fused_decode_fp8_shapes(B, Hq, Hkv, D, rot, lens):
+    """e4m3 caches at the other head sizes and group widths: the PV operand
+    layouts for 4- and 8-byte V chunks and the 4-wave kernels."""
+    announce(f"fused decode fp8 B={B} Hq={Hq} Hkv={Hkv} D={D} lens={lens}")
+    case = make_decode_case(33, B, Hq, Hkv, D, rot, lens, fp8=True)
+    out, cache = run_fused(case)
+    ref, _, v_ref, _, _ = oracle_decode(case, codec="ocp")
+    check(out, ref, TOL_FP8, "fused fp8 shapes")
+    for b, p in enumerate(lens):
+        assert torch.equal(cache.v[b, :, p].cpu(), v_ref[b, :, p])
+
+
 def test_fused_decode_paged():
     """Config-5 style: block-paged cache of 64-token pages, G = 8, ragged lengths."""
     B, Hq, Hkv, D, rot, ps = 5, 16, 2, 256, 64, 64
