@@ -68,7 +68,7 @@ struct SkinnyParams {
 template <typename OT, bool RES, bool ROPE = false>
 __global__ __launch_bounds__(64 * kSkinnyWaves) __attribute__((amdgpu_waves_per_eu(4))) void skinny_lds_kernel(SkinnyLdsParams p, RopeEpi e) {
     __shared__ SkinnyLdsBase lds;  // no NORM staging here: two workgroups a CU
-    skinny_lds_body<OT, RES, ROPE, false, bf16_t, false, false, SkinnyLdsBase>(p, e, blockIdx.x, blockIdx.z, lds);
+    skinny_lds_body<OT, RES, ROPE, false, bf16_t, false, false, SkinnyLdsBase, false, kSkinnyLdsSteps>(p, e, blockIdx.x, blockIdx.z, lds);
 }
 
 constexpr int kSkinnyCB = 1;                        // 16-column blocks per workgroup
