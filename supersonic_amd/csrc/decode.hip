@@ -47,8 +47,13 @@
 
 namespace ssa {
 
+// The 4-wave kernels (head groups of 8 and 16) are held to two waves a SIMD
+// (235 registers instead of 300): two workgroups a CU, so the ragged plan's
+// target of 512 workgroups is resident at once (config 5's decodes 338.6 ->
+// 331 us).
 template <typename QT, bool FP8, int D, int GP>
-__global__ __launch_bounds__(64 * decode_waves(GP)) void decode_split_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * decode_waves(GP)) __attribute__((amdgpu_waves_per_eu(GP >= 8 ? 2 : 1, 2)))
+void decode_split_kernel(DecodeParams p) {
     __shared__ DecodeLds<D, GP> lds;
     decode_split_body<QT, FP8, D, GP>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
