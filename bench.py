@@ -204,6 +204,7 @@ class Workloads:
             K.fused_decode(0, args["q_proj"], args["k_new"], args["v_new"], args["qw"], args["kw"], args["cos"],
                            args["sin"], args["pos"], caches[i], args["out"], q_heads=Hq, kv_heads=Hkv,
                            head_dim=D, rotary_dim=rot, max_kv_len=max(lens) + 1, workspace=args["ws"])
+        self.last_decode = (args, caches)
         return step, n_copies
 
     def decode_result(self, name, B, lens, Hq, Hkv, D, rot, fp8=False, paged_ps=None, cap=None, traffic_key=None):
@@ -275,6 +276,8 @@ class Workloads:
         def step(i):
             K.fused_prefill(0, q_proj, k_new, v_new, qw, kw, cos, sin, cache, out, q_heads=Hq, kv_heads=Hkv,
                             head_dim=D, rotary_dim=rot, chunk_start=start)
+        self.last_prefill = {"q_proj": q_proj, "k_new": k_new, "v_new": v_new, "cache": cache, "out": out,
+                             "chunk_start": start}
         return step
 
     @staticmethod
@@ -389,8 +392,10 @@ class Workloads:
 
     def mixed(self):
         """Config 5: one 8192-token prefill chunk + 32 decode sequences, 16/2 heads,
-        paged KV with 64-token pages; the two calls run back to back on one stream."""
-        torch = self.torch
+        paged KV with 64-token pages.  The step is one mixed call (decode, then the
+        chunk); the two separate calls and the mixed call with the CU split
+        (decode on 128 workgroups, the chunk beside it) are timed beside it."""
+        torch, K = self.torch, self.K
         Hq, Hkv, D, rot = 16, 2, 256, 64
         g = torch.Generator().manual_seed(5)
         lens = torch.randint(512, 65537, (32,), generator=g).tolist()
@@ -403,18 +408,38 @@ class Workloads:
         def both(i):
             pstep(i)
             dstep(i % n)
-        tot_ms, _, _ = self.timed(both, n)
+        serial_ms, _, _ = self.timed(both, n)
+        # one mixed call: decode on a share of the CUs, the chunk beside it
+        dargs, dcaches = self.last_decode
+        chunk = self.last_prefill
+        decs = [{"q_proj": dargs["q_proj"], "k_new": dargs["k_new"], "v_new": dargs["v_new"],
+                 "positions": dargs["pos"], "cache": c, "out": dargs["out"], "max_kv_len": max(lens) + 1}
+                for c in dcaches]
+        mws = torch.zeros(K.mixed_workspace_size(False, Hq, Hkv, D, chunk, decs[0]), dtype=torch.uint8,
+                          device=self.dev)
+
+        def conc(i):
+            K.fused_mixed(0, dargs["qw"], dargs["kw"], dargs["cos"], dargs["sin"], chunk=chunk, decode=decs[i % n],
+                          q_heads=Hq, kv_heads=Hkv, head_dim=D, rotary_dim=rot, workspace=mws)
+        tot_ms, _, _ = self.timed(conc, n)
+        # the same call with the CU split (decode planned for 128 workgroups)
+        import os
+        os.environ["SUPERSONIC_MIXED_DECODE_WGS"] = "128"
+        split_ms, _, _ = self.timed(conc, n)
+        del os.environ["SUPERSONIC_MIXED_DECODE_WGS"]
         fl = self.causal_flops(8192, Hq, D)
         kv_bytes, d_bytes = self.decode_bytes(lens, Hq, Hkv, D, 2)
         self.torch.cuda.empty_cache()
-        return {"workload": "config 5, 8192-token chunk + 32 paged decode seqs (16/2 heads, pages of 64)",
-                "ms_per_step": tot_ms, "prefill_kernel_ms": p_kern, "decode_kernel_ms": d_kern,
+        return {"workload": "config 5, 8192-token chunk + 32 paged decode seqs (16/2 heads, pages of 64), "
+                            "one mixed call",
+                "ms_per_step": tot_ms, "two_calls_ms_per_step": serial_ms, "cu_split_ms_per_step": split_ms,
+                "prefill_kernel_ms": p_kern, "decode_kernel_ms": d_kern,
                 "prefill_tflops": fl / (p_kern * 1e-3) / 1e12,
                 "prefill_frac": fl / (p_kern * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 "decode_gbs": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9,
                 "decode_frac": (kv_bytes + 32 * Hq * D * 2) / (d_kern * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 # the step's combined bound max(bytes / HBM peak, flops / MFMA peak)
-                # against the measured step (the two calls run one after the other)
+                # against the measured step (one mixed call)
                 "combined_bound_ms": max((kv_bytes + 32 * Hq * D * 2) / (HBM_PEAK_GBS * 1e9),
                                          fl / (BF16_PEAK_TFLOPS * 1e12)) * 1e3,
                 "combined_frac": max((kv_bytes + 32 * Hq * D * 2) / (HBM_PEAK_GBS * 1e9),

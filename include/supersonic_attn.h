@@ -278,6 +278,56 @@ int supersonic_attn_gfx950_prefill(
     const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
     const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes);
 
+/* A mixed step: one prefill chunk and a batch of decode sequences of the same
+ * layer in one call (no reference counterpart: the reference runs prefill and
+ * decode as separate engine steps, prefill_engine.rs / decode_engine.rs; this
+ * serves chunked-prefill batching).  By default the decode, then the chunk,
+ * run on `stream`.  With SUPERSONIC_MIXED_DECODE_WGS = c > 0 they run at the
+ * same time on disjoint CUs: the decode first on `stream`, planned for c
+ * workgroups, the chunk on a library stream forked from `stream` (same
+ * priority) with a dynamic item schedule, so its workgroups take the CUs the
+ * decode leaves and the decode's as they free up; `stream` then waits for
+ * both (measured no faster at config 5).  Results are those of
+ * supersonic_attn_gfx950_decode and supersonic_attn_gfx950_prefill with the
+ * same arguments (the layer arguments are shared).  Either part may be empty
+ * (batch 0 / chunk_len 0).  The chunk's and the decodes' cache views may
+ * share one block-paged cache (different sequences).  workspace: NULL
+ * (library-owned) or caller device memory of at least
+ * supersonic_attn_gfx950_mixed_workspace_size() bytes, zero-filled before its
+ * first use and not written between calls.  Calls sharing the library
+ * stream of a device must not overlap. */
+typedef struct supersonic_prefill_chunk {
+    size_t chunk_len;
+    size_t chunk_start;
+    const void* q_proj;     /* [chunk_len, Hq*2D] bf16 */
+    const void* k_new;      /* [chunk_len, Hkv*D] bf16 */
+    const void* v_new;
+    const supersonic_kv_cache* cache;  /* the chunk's sequence is cache sequence 0 */
+    void* out;              /* [chunk_len, Hq*D] bf16 */
+} supersonic_prefill_chunk;
+
+typedef struct supersonic_decode_batch {
+    size_t batch;
+    size_t max_kv_len;      /* >= max(positions) + 1 */
+    const void* q_proj;     /* [batch, Hq*2D] bf16 */
+    const void* k_new;      /* [batch, Hkv*D] bf16 */
+    const void* v_new;
+    const int32_t* positions;  /* [batch] int32, device */
+    const supersonic_kv_cache* cache;
+    void* out;              /* [batch, Hq*D] bf16 */
+} supersonic_decode_batch;
+
+size_t supersonic_attn_gfx950_mixed_workspace_size(
+    int kv_dtype, size_t q_heads, size_t kv_heads, size_t head_dim,
+    const supersonic_prefill_chunk* chunk, const supersonic_decode_batch* decode);
+
+int supersonic_attn_gfx950_mixed(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim, float eps, float scale,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const supersonic_prefill_chunk* chunk, const supersonic_decode_batch* decode,
+    void* workspace, size_t workspace_bytes);
+
 /* Input RMSNorm + Q/K/V projections, before the attention:
  *   normed = bf16(hidden * rsqrt(mean(hidden^2) + eps) * (1 + input_norm_w))
  *   q_proj_out = bf16(normed . q_proj_w^T), k_out = bf16(normed . k_proj_w^T),

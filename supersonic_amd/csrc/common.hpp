@@ -8,6 +8,8 @@
 #include <stdint.h>
 #include <cstdlib>
 
+#include "supersonic_attn.h"
+
 namespace ssa {
 
 // ----------------------------------------------------------------------------
@@ -324,7 +326,8 @@ constexpr int kWorkspaceProjLt = 3;  // hipBLASLt workspace
 constexpr int kWorkspaceSkinny = 4;  // split-k partials and arrival counters of the o_proj kernel
 constexpr int kWorkspaceGemm = 5;    // tail-split partials and flags of the hand-written GEMM
 constexpr int kWorkspaceRope = 6;    // qkv_proj_rope: per-head counters (zero between calls), then rows
-constexpr int kWorkspaceSlots = 7;
+constexpr int kWorkspaceMixed = 7;   // mixed step: the prefill's claim counters (zero between calls)
+constexpr int kWorkspaceSlots = 8;
 void* device_workspace(int device, size_t bytes, int slot);
 
 // Compute units of `device` (cached; 256 on MI355X), 0 if the query fails.
@@ -365,6 +368,24 @@ static inline hipError_t take_wait_error(unsigned* bits) {
 hipError_t take_wait_error_decode(unsigned* bits);
 hipError_t take_wait_error_layer(unsigned* bits);
 hipError_t take_wait_error_gemm(unsigned* bits);
+
+// The fused entry points with their scheduling knobs (decode.hip,
+// prefill.hip): decode planned for target_wgs workgroups (0: the whole GPU),
+// prefill on the dynamic schedule when claims is not NULL (16 zeroed
+// 128-byte counter lines).
+int decode_native(size_t device_ordinal, void* stream, int kv_dtype, size_t batch, size_t q_heads,
+                  size_t kv_heads, size_t head_dim, size_t rotary_dim, size_t max_kv_len, float eps, float scale,
+                  const void* q_proj, const void* k_new, const void* v_new, const void* q_norm_w,
+                  const void* k_norm_w, const void* cos_table, const void* sin_table, const int32_t* positions,
+                  const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes,
+                  int target_wgs);
+int prefill_native(size_t device_ordinal, void* stream, int kv_dtype, size_t q_heads, size_t kv_heads,
+                   size_t head_dim, size_t rotary_dim, size_t chunk_len, size_t chunk_start, float eps, float scale,
+                   const void* q_proj, const void* k_new, const void* v_new, const void* q_norm_w,
+                   const void* k_norm_w, const void* cos_table, const void* sin_table,
+                   const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes,
+                   unsigned* claims);
+constexpr size_t kClaimBytes = 16 * 128;
 
 // Row repack with cast and zero padding (elementwise.hip): dst row
 // (o, i) of dout elements = src[o * so + i * si + 0 .. din) cast from dtype

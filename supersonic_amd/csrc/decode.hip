@@ -157,6 +157,7 @@ struct DecodeRequest {
     int device;
     hipStream_t stream;
     bool ragged;      // per-sequence lengths: plan on the device from the lengths
+    int target;       // ragged plan: workgroups to plan for (0: one round on the whole GPU)
 };
 
 // Returns 0, or a SUPERSONIC_ERR_* status.
@@ -188,7 +189,7 @@ static int run_decode(DecodeRequest& r) {
     p.nsplit = sp.nsplit;
     p.ragged = r.ragged ? 1 : 0;
     p.B = r.B;
-    p.target = decode_target(waves);
+    p.target = r.ragged && r.target > 0 ? std::min(r.target, decode_target(waves)) : decode_target(waves);
     p.min_chunk = decode_min_chunk();
     p.det = decode_deterministic();
     p.scale_log2 = r.scale * kLog2e;
@@ -380,14 +381,14 @@ static int check_sizes(size_t a, size_t b, size_t c, size_t d, size_t e) {
     return (a > lim || b > lim || c > lim || d > lim || e > lim) ? SUPERSONIC_ERR_RANGE : 0;
 }
 
-extern "C" int supersonic_attn_gfx950_decode(
-    size_t device_ordinal, void* stream, int kv_dtype,
-    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
-    size_t max_kv_len, float eps, float scale,
-    const void* q_proj, const void* k_new, const void* v_new,
-    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
-    const int32_t* positions, const supersonic_kv_cache* cache, void* out,
-    void* workspace, size_t workspace_bytes) {
+// The fused decode planned for `target_wgs` workgroups (0: the whole GPU);
+// supersonic_attn_gfx950_decode is the whole-GPU one.
+int ssa::decode_native(size_t device_ordinal, void* stream, int kv_dtype, size_t batch, size_t q_heads,
+                  size_t kv_heads, size_t head_dim, size_t rotary_dim, size_t max_kv_len, float eps, float scale,
+                  const void* q_proj, const void* k_new, const void* v_new, const void* q_norm_w,
+                  const void* k_norm_w, const void* cos_table, const void* sin_table, const int32_t* positions,
+                  const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes,
+                  int target_wgs) {
     if (kv_dtype != SUPERSONIC_KV_BF16 && kv_dtype != SUPERSONIC_KV_FP8_E4M3) return SUPERSONIC_ERR_DTYPE;
     if (int rc = check_sizes(batch, q_heads, kv_heads, head_dim, max_kv_len)) return rc;
     if (!q_proj || !k_new || !v_new || !q_norm_w || !k_norm_w || !positions || !out) return SUPERSONIC_ERR_NULL;
@@ -430,7 +431,21 @@ extern "C" int supersonic_attn_gfx950_decode(
     p.sin_t = static_cast<const uint16_t*>(sin_table);
     p.half_rot = static_cast<int>(rotary_dim / 2);
     p.eps = eps;
+    r.target = target_wgs;
     return run_decode(r);
+}
+
+extern "C" int supersonic_attn_gfx950_decode(
+    size_t device_ordinal, void* stream, int kv_dtype,
+    size_t batch, size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
+    size_t max_kv_len, float eps, float scale,
+    const void* q_proj, const void* k_new, const void* v_new,
+    const void* q_norm_w, const void* k_norm_w, const void* cos_table, const void* sin_table,
+    const int32_t* positions, const supersonic_kv_cache* cache, void* out,
+    void* workspace, size_t workspace_bytes) {
+    return decode_native(device_ordinal, stream, kv_dtype, batch, q_heads, kv_heads, head_dim, rotary_dim, max_kv_len,
+                         eps, scale, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table, sin_table, positions, cache,
+                         out, workspace, workspace_bytes, 0);
 }
 
 // ----------------------------------------------------------------------------

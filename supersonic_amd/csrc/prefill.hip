@@ -45,6 +45,11 @@ struct PrefillParams {
     int nqt;             // query tiles of 128 rows
     int B;               // sequences
     int n_wg;            // workgroups of the persistent grid
+    // Dynamic schedule (NULL: the static one).  Per item list x (an XCD's, or
+    // the single list) a claim counter at claims[32 x] and a finished-workgroup
+    // counter at claims[32 (8 + x)], each on its own 128-byte line; both are
+    // zero before a launch and the list's last workgroup to finish zeroes them.
+    unsigned* claims;
     // drop-in output: f32, element (b, h, row, d) at b*o_bs + h*o_hs + row*o_rs + d
     float* out_f32;
     int64_t o_bs, o_hs, o_rs;
@@ -203,10 +208,25 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const int W = by_xcd ? (p.n_wg >> 3) : p.n_wg;
     const int hpi = by_xcd ? hpx : p.Hq;     // heads per item list
     const int n_items = p.nqt * hpi * p.B;
+    // Dynamic schedule: the list's items are claimed one at a time from a
+    // counter in list order (longest first), so workgroups that start late
+    // (their CUs busy with other work when the grid was dispatched) take only
+    // what is left.  The first copy wave claims item r + 1 as item r starts
+    // and leaves it in claimed[(r + 1) & 1]; every reader is at least one
+    // workgroup barrier behind the write.
+    __shared__ int claimed[2];
+    const bool dyn = p.claims != nullptr;
+    unsigned* const ctr = dyn ? p.claims + 32 * (by_xcd ? (bid & 7) : 0) : nullptr;
+    auto claim_next = [&](const int slot) {
+        if (wave == kPrefillWaves && (tid & 63) == 0) {
+            claimed[slot] = static_cast<int>(__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the write is in LDS before the next barrier
+        }
+    };
     // Item r of this workgroup (false past the last): 128 query rows `qt` of
-    // head h of sequence b.  The sequence of m is increasing.
+    // head h of sequence b.  The sequence of m is increasing (static schedule).
     auto item_at = [&](const int r, int& qt, int& h, int& b) -> bool {
-        const int m = (r & 1) ? (r + 1) * W - 1 - j : r * W + j;
+        const int m = dyn ? claimed[r & 1] : ((r & 1) ? (r + 1) * W - 1 - j : r * W + j);
         if (m >= n_items) return false;
         qt = p.nqt - 1 - m / (hpi * p.B);
         const int rem = m % (hpi * p.B);
@@ -267,15 +287,18 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         // first tile of the first item that has keys at all
         auto issue_first = [&](int r, const int st) {
             int qt, h, b;
-            for (; item_at(r, qt, h, b); ++r)
+            for (; item_at(r, qt, h, b); ++r) {
                 if (tiles_of(qt) > 0) {
                     issue_tile(h, b, 0, st);
                     return;
                 }
+                if (dyn) return;  // only item r is claimed yet (and every item has tiles)
+            }
         };
         issue_first(0, 1);
         int gt = 0, qt, h, b;
         for (int r = 0; item_at(r, qt, h, b); ++r) {
+            if (dyn) claim_next((r + 1) & 1);
             const int nt = tiles_of(qt);
             for (int it = 0; it < nt; ++it) {
                 // Tile `it` has landed.  The compute waves' barrier also
@@ -290,6 +313,16 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
             gt += nt;
         }
         wait_vm0();  // no LDS write in flight when the workgroup ends
+        if (dyn && wave == kPrefillWaves && (tid & 63) == 0) {
+            // This workgroup's claims are over (its last one failed); the
+            // list's last workgroup to get here leaves both counters at zero.
+            unsigned* const done = ctr + 32 * 8;
+            const unsigned wl = by_xcd ? static_cast<unsigned>(p.n_wg >> 3) : static_cast<unsigned>(p.n_wg);
+            if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == wl) {
+                __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
     };
     // One work item = 128 query rows of one head of one sequence, run by the
     // compute waves; gt = tiles of the workgroup's items before it.  A
@@ -602,6 +635,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
 
     // Separate loops for the copy and the compute waves (same items, same
     // barrier count per item), so neither keeps the other's registers live.
+    if (dyn) {
+        claim_next(0);
+        __builtin_amdgcn_s_barrier();  // item 0's claim is visible to every wave
+    }
     if (wave >= kPrefillWaves) {
         copy_items();
     } else {
@@ -1021,11 +1058,16 @@ extern "C" size_t supersonic_attn_gfx950_prefill_workspace_size(int kv_dtype, si
     return kv_dtype == SUPERSONIC_KV_FP8_E4M3 ? 2 * stage : stage;  // + the bf16 K rows of an fp8 cache
 }
 
-extern "C" int supersonic_attn_gfx950_prefill(
-    size_t device_ordinal, void* stream, int kv_dtype, size_t q_heads, size_t kv_heads, size_t head_dim,
-    size_t rotary_dim, size_t chunk_len, size_t chunk_start, float eps, float scale, const void* q_proj,
-    const void* k_new, const void* v_new, const void* q_norm_w, const void* k_norm_w, const void* cos_table,
-    const void* sin_table, const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes) {
+namespace ssa {
+// The fused prefill with an optional dynamic schedule (claims: zeroed claim
+// counters, PrefillParams::claims); supersonic_attn_gfx950_prefill is the
+// static one.
+int prefill_native(size_t device_ordinal, void* stream, int kv_dtype, size_t q_heads, size_t kv_heads,
+                   size_t head_dim, size_t rotary_dim, size_t chunk_len, size_t chunk_start, float eps, float scale,
+                   const void* q_proj, const void* k_new, const void* v_new, const void* q_norm_w,
+                   const void* k_norm_w, const void* cos_table, const void* sin_table,
+                   const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes,
+                   unsigned* claims) {
     if (kv_dtype != SUPERSONIC_KV_BF16 && kv_dtype != SUPERSONIC_KV_FP8_E4M3) return SUPERSONIC_ERR_DTYPE;
     const bool fp8 = kv_dtype == SUPERSONIC_KV_FP8_E4M3;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return SUPERSONIC_ERR_HEAD_DIM;
@@ -1065,6 +1107,7 @@ extern "C" int supersonic_attn_gfx950_prefill(
     p.half_rot = static_cast<int>(rotary_dim / 2);
     p.eps = eps;
     p.B = 1;
+    p.claims = claims;
     // K norm + RoPE + cache append for the chunk and the V^T staging of every
     // position, in one pass
     {
@@ -1125,4 +1168,15 @@ extern "C" int supersonic_attn_gfx950_prefill(
         return SUPERSONIC_ERR_LAUNCH;
     if (prof.after) (void)hipEventRecord(prof.after, st);
     return 0;
+}
+}  // namespace ssa
+
+extern "C" int supersonic_attn_gfx950_prefill(
+    size_t device_ordinal, void* stream, int kv_dtype, size_t q_heads, size_t kv_heads, size_t head_dim,
+    size_t rotary_dim, size_t chunk_len, size_t chunk_start, float eps, float scale, const void* q_proj,
+    const void* k_new, const void* v_new, const void* q_norm_w, const void* k_norm_w, const void* cos_table,
+    const void* sin_table, const supersonic_kv_cache* cache, void* out, void* workspace, size_t workspace_bytes) {
+    return ssa::prefill_native(device_ordinal, stream, kv_dtype, q_heads, kv_heads, head_dim, rotary_dim, chunk_len,
+                               chunk_start, eps, scale, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table,
+                               sin_table, cache, out, workspace, workspace_bytes, nullptr);
 }

@@ -68,6 +68,21 @@ _p = C.c_void_p
 _i = C.c_int
 _f = C.c_float
 
+
+class PrefillChunkDesc(C.Structure):
+    """``supersonic_prefill_chunk`` (include/supersonic_attn.h)."""
+    _fields_ = [("chunk_len", C.c_size_t), ("chunk_start", C.c_size_t), ("q_proj", C.c_void_p),
+                ("k_new", C.c_void_p), ("v_new", C.c_void_p), ("cache", C.POINTER(KvCacheDesc)),
+                ("out", C.c_void_p)]
+
+
+class DecodeBatchDesc(C.Structure):
+    """``supersonic_decode_batch`` (include/supersonic_attn.h)."""
+    _fields_ = [("batch", C.c_size_t), ("max_kv_len", C.c_size_t), ("q_proj", C.c_void_p),
+                ("k_new", C.c_void_p), ("v_new", C.c_void_p), ("positions", C.c_void_p),
+                ("cache", C.POINTER(KvCacheDesc)), ("out", C.c_void_p)]
+
+
 SIGNATURES = {
     "supersonic_qwen35_hip_full_attention_prefill":
         [_i, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f, _sz, _p, _p, _p, _p],
@@ -100,6 +115,11 @@ SIGNATURES = {
     "supersonic_attn_gfx950_prefill":
         [_sz, _p, _i, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
          _p, _p, _p, _p, _p, _p, _p, C.POINTER(KvCacheDesc), _p, _p, _sz],
+    "supersonic_attn_gfx950_mixed_workspace_size":
+        [_i, _sz, _sz, _sz, C.POINTER(PrefillChunkDesc), C.POINTER(DecodeBatchDesc)],
+    "supersonic_attn_gfx950_mixed":
+        [_sz, _p, _i, _sz, _sz, _sz, _sz, _f, _f, _p, _p, _p, _p, C.POINTER(PrefillChunkDesc),
+         C.POINTER(DecodeBatchDesc), _p, _sz],
     "supersonic_attn_gfx950_o_proj_workspace_size": [_sz, _sz, _sz],
     "supersonic_attn_gfx950_o_proj_residual": [_sz, _p, _i, _sz, _sz, _sz, _p, _p, _p, _p, _sz],
     "supersonic_attn_gfx950_qkv_proj_workspace_size": [_sz, _sz, _sz, _sz],
@@ -119,7 +139,7 @@ SIGNATURES = {
     "supersonic_attn_rope_tables": [_sz, _sz, C.c_double, _p, _p],
     "supersonic_attn_version": [],
 }
-RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_gfx950_prefill_workspace_size": _sz,
+RESTYPES = {"supersonic_attn_gfx950_decode_workspace_size": _sz, "supersonic_attn_gfx950_mixed_workspace_size": _sz, "supersonic_attn_gfx950_prefill_workspace_size": _sz,
             "supersonic_attn_gfx950_o_proj_workspace_size": _sz, "supersonic_attn_gfx950_qkv_proj_workspace_size": _sz,
             "supersonic_attn_gfx950_qkv_proj_rope_workspace_size": _sz,
             "supersonic_attn_gfx950_decode_layer_workspace_size": _sz, "supersonic_attn_version": C.c_char_p,
@@ -378,6 +398,47 @@ def fused_prefill(ordinal, q_proj, k_new, v_new, q_norm_w, k_norm_w, cos_table, 
         rotary_dim, S, chunk_start, eps, scale, _ptr(q_proj), _ptr(k_new), _ptr(v_new), _ptr(q_norm_w),
         _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), C.byref(desc), _ptr(out), *_ws(workspace))
     _check("fused_prefill", st)
+
+
+def _mixed_descs(chunk, decode):
+    """ctypes descriptors (and the cache descriptors they point at) of a mixed step."""
+    keep = []
+    cd = dd = None
+    if chunk is not None:
+        cdesc = chunk["cache"].desc()
+        keep.append(cdesc)
+        cd = PrefillChunkDesc(chunk["q_proj"].shape[0], chunk.get("chunk_start", 0), _ptr(chunk["q_proj"]),
+                              _ptr(chunk["k_new"]), _ptr(chunk["v_new"]), C.pointer(cdesc), _ptr(chunk["out"]))
+    if decode is not None:
+        ddesc = decode["cache"].desc()
+        keep.append(ddesc)
+        dd = DecodeBatchDesc(decode["q_proj"].shape[0], decode["max_kv_len"], _ptr(decode["q_proj"]),
+                             _ptr(decode["k_new"]), _ptr(decode["v_new"]), _ptr(decode["positions"]),
+                             C.pointer(ddesc), _ptr(decode["out"]))
+    return cd, dd, keep
+
+
+def mixed_workspace_size(fp8, q_heads, kv_heads, head_dim, chunk=None, decode=None) -> int:
+    cd, dd, _keep = _mixed_descs(chunk, decode)
+    return int(load().supersonic_attn_gfx950_mixed_workspace_size(
+        KV_FP8_E4M3 if fp8 else KV_BF16, q_heads, kv_heads, head_dim, C.byref(cd) if cd else None,
+        C.byref(dd) if dd else None))
+
+
+def fused_mixed(ordinal, q_norm_w, k_norm_w, cos_table, sin_table, *, chunk=None, decode=None, q_heads, kv_heads,
+                head_dim, rotary_dim, eps=1e-6, scale=None, stream=None, workspace=None):
+    """``supersonic_attn_gfx950_mixed``: a prefill chunk and a decode batch of one layer at the same time.
+
+    ``chunk``: dict(q_proj, k_new, v_new, cache, out, chunk_start); ``decode``: dict(q_proj, k_new, v_new,
+    positions, cache, out, max_kv_len).  The results are those of ``fused_prefill`` and ``fused_decode``."""
+    scale = head_dim ** -0.5 if scale is None else scale
+    cd, dd, _keep = _mixed_descs(chunk, decode)
+    fp8 = (chunk or decode)["cache"].fp8
+    st = load().supersonic_attn_gfx950_mixed(
+        ordinal, _stream_ptr(stream), KV_FP8_E4M3 if fp8 else KV_BF16, q_heads, kv_heads, head_dim, rotary_dim, eps,
+        scale, _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos_table), _ptr(sin_table), C.byref(cd) if cd else None,
+        C.byref(dd) if dd else None, *_ws(workspace))
+    _check("fused_mixed", st)
 
 
 def o_proj_residual(ordinal, attn, o_proj_w, hidden, stream=None, workspace=None):

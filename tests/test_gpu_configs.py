@@ -88,11 +88,16 @@ def test_config4_fp8_batch16_ragged():
         assert torch.equal(cache.v_scale[b, :, p].cpu(), vs_ref[b, :, p])
 
 
-def test_config5_mixed_paged_batch():
+@pytest.mark.parametrize("mode", ["serial", "concurrent"])
+def test_config5_mixed_paged_batch(mode, monkeypatch):
     """Config 5: 16/2 heads, D 256, bf16, one block-paged pool of 64-token pages
     holding an 8192-token prefill chunk (offset 0) and 32 decode sequences with
-    the benchmark's lengths (seed 5, U[512, 65536]); prefill then decode on one
-    stream, both checked against the oracle."""
+    the benchmark's lengths (seed 5, U[512, 65536]), both checked against the
+    oracle.  serial: prefill then decode on one stream.  concurrent: one mixed
+    call with the CU split (decode planned for 96 workgroups, the chunk on a
+    second stream with the dynamic schedule), made twice on a caller
+    workspace: the second call gives the same chunk output bit for bit and
+    leaves the claim counters at zero."""
     Hq, Hkv, D, rot, ps, S = 16, 2, 256, 64, 64, 8192
     lens = torch.randint(512, 65537, (32,), generator=torch.Generator().manual_seed(5)).tolist()
     B = len(lens)
@@ -147,10 +152,33 @@ def test_config5_mixed_paged_batch():
     args_d = {"q_proj": qp_d.to(DEV), "k_new": kn_d.to(DEV), "v_new": vn_d.to(DEV), "qw": qw_d, "kw": kw_d,
               "cos": cos_d, "sin": sin_d, "pos": pos.to(DEV)}
     torch.cuda.synchronize()
-    K.fused_prefill(0, *args_c, qw_d, kw_d, cos_d, sin_d, chunk_cache, out_c, q_heads=Hq, kv_heads=Hkv,
-                    head_dim=D, rotary_dim=rot, chunk_start=0, stream=st)
-    out_d = fused_decode(args_d, dec_cache, B, Hq, Hkv, D, rot, max(lens) + 1, stream=st)
-    st.synchronize()
+    if mode == "serial":
+        K.fused_prefill(0, *args_c, qw_d, kw_d, cos_d, sin_d, chunk_cache, out_c, q_heads=Hq, kv_heads=Hkv,
+                        head_dim=D, rotary_dim=rot, chunk_start=0, stream=st)
+        out_d = fused_decode(args_d, dec_cache, B, Hq, Hkv, D, rot, max(lens) + 1, stream=st)
+        st.synchronize()
+    else:
+        out_d = torch.full((B, Hq * D), float("nan"), dtype=torch.bfloat16, device=DEV)
+        chunk = {"q_proj": args_c[0], "k_new": args_c[1], "v_new": args_c[2], "cache": chunk_cache, "out": out_c,
+                 "chunk_start": 0}
+        dec = {"q_proj": args_d["q_proj"], "k_new": args_d["k_new"], "v_new": args_d["v_new"],
+               "positions": args_d["pos"], "cache": dec_cache, "out": out_d, "max_kv_len": max(lens) + 1}
+        ws = torch.zeros(K.mixed_workspace_size(False, Hq, Hkv, D, chunk, dec), dtype=torch.uint8, device=DEV)
+        monkeypatch.setenv("SUPERSONIC_MIXED_DECODE_WGS", "96")
+        K.fused_mixed(0, qw_d, kw_d, cos_d, sin_d, chunk=chunk, decode=dec, q_heads=Hq, kv_heads=Hkv, head_dim=D,
+                      rotary_dim=rot, stream=st, workspace=ws)
+        st.synchronize()
+        assert int(ws[:2048].count_nonzero()) == 0, "claim counters not left at zero"
+        first_c = out_c.clone()
+        first_d = out_d.clone()
+        out_c.fill_(float("nan"))
+        K.fused_mixed(0, qw_d, kw_d, cos_d, sin_d, chunk=chunk, decode=dec, q_heads=Hq, kv_heads=Hkv, head_dim=D,
+                      rotary_dim=rot, stream=st, workspace=ws)
+        st.synchronize()
+        monkeypatch.delenv("SUPERSONIC_MIXED_DECODE_WGS")
+        assert int(ws[:2048].count_nonzero()) == 0, "claim counters not left at zero"
+        assert torch.equal(out_c, first_c), "second mixed call: chunk output differs"
+        check(out_d, first_d.float().cpu(), TOL_BF16, "config5 decode, second mixed call")
 
     # decode sequences against the oracle
     ref_d = O.decode_layer(shape, qp_d, kn_d, vn_d, qw, kw, cos, sin, pos.long(), k_host, v_host)
