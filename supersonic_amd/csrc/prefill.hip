@@ -211,8 +211,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     // Dynamic schedule: the list's items are claimed one at a time from a
     // counter in list order (longest first), so workgroups that start late
     // (their CUs busy with other work when the grid was dispatched) take only
-    // what is left.  The first copy wave claims item r + 1 as item r starts
-    // and leaves it in claimed[(r + 1) & 1]; every reader is at least one
+    // what is left.  The first copy wave claims item r + 1 during item r and
+    // leaves it in claimed[(r + 1) & 1]; every reader is at least one
     // workgroup barrier behind the write.
     __shared__ int claimed[2];
     const bool dyn = p.claims != nullptr;
@@ -298,14 +298,20 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
         issue_first(0, 1);
         int gt = 0, qt, h, b;
         for (int r = 0; item_at(r, qt, h, b); ++r) {
-            if (dyn) claim_next((r + 1) & 1);
             const int nt = tiles_of(qt);
+            // The next item is claimed as this one nears its end (at the
+            // barrier of tile nt - 3, two barriers before the other copy
+            // waves read the claim), so workgroups claim in the order they
+            // finish: longest-processing-time-first.  Items of fewer than 3
+            // tiles claim at their start.
+            if (dyn && nt < 3) claim_next((r + 1) & 1);
             for (int it = 0; it < nt; ++it) {
                 // Tile `it` has landed.  The compute waves' barrier also
                 // orders their LDS reads; these waves read no LDS, so a bare
                 // barrier (no implied wait for every load in flight) is enough.
                 wait_vm0();
                 __builtin_amdgcn_s_barrier();
+                if (dyn && nt >= 3 && it == nt - 3) claim_next((r + 1) & 1);
                 if (it + 1 < nt) issue_tile(h, b, it + 1, (gt + it + 2) & 1);
                 else issue_first(r + 1, (gt + nt + 1) & 1);
             }
