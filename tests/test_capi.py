@@ -127,6 +127,26 @@ def test_projection_entry_validation(lib):
     assert qkv(2, 0) == K.ERR["RANGE"]
 
 
+def test_mixed_workspace_size_is_host_only(lib):
+    """The mixed step's workspace: 2 KiB of claim counters, then the decode's and the
+    chunk's workspaces, each rounded up to 256 bytes (no GPU call; the tensors are
+    only read for their shapes and pointers)."""
+    import torch
+    Hq, Hkv, D, S, B = 16, 2, 256, 300, 3
+    cache = K.KvCache(torch.zeros(1, Hkv, 8, D, dtype=torch.bfloat16), torch.zeros(1, Hkv, 8, D, dtype=torch.bfloat16))
+    chunk = {"q_proj": torch.zeros(S, 1), "k_new": None, "v_new": None, "cache": cache, "out": None,
+             "chunk_start": 40}
+    dec = {"q_proj": torch.zeros(B, 1), "k_new": None, "v_new": None, "positions": None, "cache": cache,
+           "out": None, "max_kv_len": 5000}
+    r256 = lambda n: (n + 255) // 256 * 256
+    dws = r256(K.decode_workspace_size(B, Hq, Hkv, D, 5000))
+    pws = r256(K.prefill_workspace_size(False, Hkv, D, S, 40))
+    assert K.mixed_workspace_size(False, Hq, Hkv, D, chunk, dec) == 2048 + dws + pws
+    assert K.mixed_workspace_size(False, Hq, Hkv, D, chunk, None) == 2048 + pws
+    assert K.mixed_workspace_size(False, Hq, Hkv, D, None, dec) == 2048 + dws
+    assert K.mixed_workspace_size(False, Hq, Hkv, D, None, None) == 2048
+
+
 def test_workspace_size_is_host_only(lib):
     n = K.decode_workspace_size(1, 16, 4, 256, 32769)
     assert n > 16 * 256 * 4
