@@ -359,94 +359,185 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int s = 0; s < KS; ++s)
             qb[s] = to_op<op_t>(row_ok ? ld16(qrow + 32 * s + 8 * g4) : u32x4_v{0u, 0u, 0u, 0u});
-    } else {
-        // This wave's 16 query rows: RMSNorm with (1 + w) and rotate-half RoPE
-        // at position off + row, bf16 after each step (prefill_engine.rs:2025-2096),
-        // (lane c of a row holds dims 8c .. 8c+7); every global load is issued
-        // before any arithmetic.  The rows are staged in LDS (stage 0), where
-        // the RoPE partner dims are read back and the operand is read
-        // transposed.
-        uint16_t* qs = reinterpret_cast<uint16_t*>(lds + (gt & 1) * T::STAGE) + wave * 16 * D;
-        constexpr int LPR = D / 8;              // lanes per row, 16 B each
-        constexpr int RPI = 64 / LPR;           // rows per instruction
-        constexpr int NIN = 16 / RPI;           // instructions per wave
-        const int c = lane % LPR, rr = lane / LPR;
-        const int hr = p.half_rot;              // a multiple of 16 (checked on the host)
-        const bool rot = 8 * c < 2 * hr;
-        const u32x4_v wtw = ld16(p.q_norm_w + 8 * c);
-        u32x4_v qw[NIN], cw[NIN], sw[NIN];
+    } else if (p.half_rot % 32 == 0 || p.half_rot == 16) {
+        // This wave's 16 query rows normed and rotated in the operand layout
+        // itself: lane holds row myrow, dims 32 s + 8 g4 + j (64 of the row's
+        // dims), RMSNorm with (1 + w) over the row (the four lanes l, l ^ 16,
+        // l ^ 32, l ^ 48 hold it), then rotate-half RoPE at position off + row,
+        // bf16 after each step (prefill_engine.rs:2025-2096).  A RoPE partner
+        // (dim d +- half_rot) is in the same lane, chunk s +- half_rot / 32,
+        // when half_rot is a multiple of 32, or in lane ^ 32, same chunk, when
+        // it is 16.  Every global load is issued before any arithmetic.
+        const int hr = p.half_rot;
+        const int hs = hr / 32;                  // rotary chunks per half (0 for half_rot 16)
+        const int pos = off + (row_ok ? myrow : 0);
+        const uint16_t* qrow = p.q + h * p.q_hs + static_cast<int64_t>(row_ok ? myrow : 0) * p.q_rs;
+        u32x4_v raw[KS], wv[KS], cw[KS / 2], sw[KS / 2];
 #pragma unroll
-        for (int k = 0; k < NIN; ++k) {
-            const int row = row_w0 + k * RPI + rr;
-            qw[k] = cw[k] = sw[k] = u32x4_v{0u, 0u, 0u, 0u};
-            if (row < S) {
-                qw[k] = ld16(p.q + h * p.q_hs + static_cast<int64_t>(row) * p.q_rs + 8 * c);
-                if (rot) {
-                    const int64_t ti = static_cast<int64_t>(off + row) * hr + (8 * c < hr ? 8 * c : 8 * c - hr);
-                    cw[k] = ld16(p.cos_t + ti);
-                    sw[k] = ld16(p.sin_t + ti);
-                }
+        for (int s = 0; s < KS; ++s) {
+            raw[s] = row_ok ? ld16(qrow + 32 * s + 8 * g4) : u32x4_v{0u, 0u, 0u, 0u};
+            wv[s] = ld16(p.q_norm_w + 32 * s + 8 * g4);
+        }
+#pragma unroll
+        for (int c = 0; c < KS / 2; ++c) {
+            cw[c] = sw[c] = u32x4_v{0u, 0u, 0u, 0u};
+            const int ci = hr == 16 ? 8 * (g4 & 1) : 32 * c + 8 * g4;  // table column of the chunk
+            if (c < (hr == 16 ? 1 : hs)) {
+                cw[c] = ld16(p.cos_t + static_cast<int64_t>(pos) * hr + ci);
+                sw[c] = ld16(p.sin_t + static_cast<int64_t>(pos) * hr + ci);
             }
         }
-        float wt[8];
-        unpack8<bf16_t>(wtw, wt);
-        // RMSNorm: the row's sum of squares over its LPR lanes on the VALU
-        // (DPP within 16 lanes, a permlane swap across 16), no LDS traffic.
-        u32x4_v nq[NIN];
+        float ss = 0.f;
 #pragma unroll
-        for (int k = 0; k < NIN; ++k) {
+        for (int s = 0; s < KS; ++s) {
             float x[8];
-            unpack8<bf16_t>(qw[k], x);
-            float ss = 0.f;
+            unpack8<bf16_t>(raw[s], x);
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
-            if constexpr (LPR >= 16) {
-                ss = row16_sum(ss);
-                if constexpr (LPR == 32) ss = xor16_sum(ss);
-            } else {
+        }
+        ss = xor32_sum(xor16_sum(ss));
+        const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
+        u32x4_v nq[KS];
 #pragma unroll
-                for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
-            }
-            const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
+        for (int s = 0; s < KS; ++s) {
+            float x[8], w[8];
+            unpack8<bf16_t>(raw[s], x);
+            unpack8<bf16_t>(wv[s], w);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                nq[k][j] = cvt_pk<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
-            st16(qs + (k * RPI + rr) * D + 8 * c, nq[k]);
+                nq[s][j] = cvt_pk<bf16_t>(x[2 * j] * inv * (w[2 * j] + 1.0f), x[2 * j + 1] * inv * (w[2 * j + 1] + 1.0f));
         }
-        if (hr > 0) {
-            // RoPE: the rotating lanes read their partner's 8 normed dims back
-            // (all reads are issued before any write; LDS is in order per wave).
+        // out = x cos + sg y sin on the normed bf16 values (sg = -1 in the first half)
+        auto rot8 = [&](const u32x4_v& xv, const u32x4_v& yv, const u32x4_v& cv, const u32x4_v& sv, const float sg) {
+            float x[8], y[8], cs[8], sn[8];
+            unpack8<bf16_t>(xv, x);
+            unpack8<bf16_t>(yv, y);
+            unpack8<bf16_t>(cv, cs);
+            unpack8<bf16_t>(sv, sn);
+            u32x4_v o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = cvt_pk<bf16_t>(x[2 * j] * cs[2 * j] + sg * y[2 * j] * sn[2 * j],
+                                      x[2 * j + 1] * cs[2 * j + 1] + sg * y[2 * j + 1] * sn[2 * j + 1]);
+            return o;
+        };
+        // chunks s < 2 HS rotate with partner chunk s +- HS (a compile-time
+        // index for each HS, so the arrays stay in registers)
+        auto rope_hs = [&](auto hs_c) {
+            constexpr int HS = decltype(hs_c)::value;
+            u32x4_v o[2 * HS];
+#pragma unroll
+            for (int s = 0; s < 2 * HS; ++s)
+                o[s] = s < HS ? rot8(nq[s], nq[s + HS], cw[s], sw[s], -1.0f)
+                              : rot8(nq[s], nq[s - HS], cw[s - HS], sw[s - HS], 1.0f);
+#pragma unroll
+            for (int s = 0; s < 2 * HS; ++s) nq[s] = o[s];
+        };
+        if (hr == 16) {
+            u32x4_v y;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(nq[0][j]), 32));
+            nq[0] = rot8(nq[0], y, cw[0], sw[0], g4 < 2 ? -1.0f : 1.0f);
+        } else {
+            static_assert(KS / 2 <= 4, "head_dim up to 256");
+            switch (hs) {
+            case 1: rope_hs(std::integral_constant<int, 1>{}); break;
+            case 2: if constexpr (KS / 2 >= 2) rope_hs(std::integral_constant<int, 2>{}); break;
+            case 3: if constexpr (KS / 2 >= 3) rope_hs(std::integral_constant<int, 3>{}); break;
+            case 4: if constexpr (KS / 2 >= 4) rope_hs(std::integral_constant<int, 4>{}); break;
+            default: break;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(nq[s]);
+    } else {
+            // This wave's 16 query rows: RMSNorm with (1 + w) and rotate-half RoPE
+            // at position off + row, bf16 after each step (prefill_engine.rs:2025-2096),
+            // (lane c of a row holds dims 8c .. 8c+7); every global load is issued
+            // before any arithmetic.  The rows are staged in LDS (stage 0), where
+            // the RoPE partner dims are read back and the operand is read
+            // transposed.
+            uint16_t* qs = reinterpret_cast<uint16_t*>(lds + (gt & 1) * T::STAGE) + wave * 16 * D;
+            constexpr int LPR = D / 8;              // lanes per row, 16 B each
+            constexpr int RPI = 64 / LPR;           // rows per instruction
+            constexpr int NIN = 16 / RPI;           // instructions per wave
+            const int c = lane % LPR, rr = lane / LPR;
+            const int hr = p.half_rot;              // a multiple of 16 (checked on the host)
+            const bool rot = 8 * c < 2 * hr;
+            const u32x4_v wtw = ld16(p.q_norm_w + 8 * c);
+            u32x4_v qw[NIN], cw[NIN], sw[NIN];
+    #pragma unroll
+            for (int k = 0; k < NIN; ++k) {
+                const int row = row_w0 + k * RPI + rr;
+                qw[k] = cw[k] = sw[k] = u32x4_v{0u, 0u, 0u, 0u};
+                if (row < S) {
+                    qw[k] = ld16(p.q + h * p.q_hs + static_cast<int64_t>(row) * p.q_rs + 8 * c);
+                    if (rot) {
+                        const int64_t ti = static_cast<int64_t>(off + row) * hr + (8 * c < hr ? 8 * c : 8 * c - hr);
+                        cw[k] = ld16(p.cos_t + ti);
+                        sw[k] = ld16(p.sin_t + ti);
+                    }
+                }
+            }
+            float wt[8];
+            unpack8<bf16_t>(wtw, wt);
+            // RMSNorm: the row's sum of squares over its LPR lanes on the VALU
+            // (DPP within 16 lanes, a permlane swap across 16), no LDS traffic.
+            u32x4_v nq[NIN];
+    #pragma unroll
+            for (int k = 0; k < NIN; ++k) {
+                float x[8];
+                unpack8<bf16_t>(qw[k], x);
+                float ss = 0.f;
+    #pragma unroll
+                for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+                if constexpr (LPR >= 16) {
+                    ss = row16_sum(ss);
+                    if constexpr (LPR == 32) ss = xor16_sum(ss);
+                } else {
+    #pragma unroll
+                    for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
+                }
+                const float inv = rsqrtf(ss / static_cast<float>(D) + p.eps);
+    #pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    nq[k][j] = cvt_pk<bf16_t>(x[2 * j] * inv * (wt[2 * j] + 1.0f), x[2 * j + 1] * inv * (wt[2 * j + 1] + 1.0f));
+                st16(qs + (k * RPI + rr) * D + 8 * c, nq[k]);
+            }
+            if (hr > 0) {
+                // RoPE: the rotating lanes read their partner's 8 normed dims back
+                // (all reads are issued before any write; LDS is in order per wave).
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int pc = 8 * c < hr ? 8 * c + hr : 8 * c - hr;
+                u32x4_v yq[NIN];
+    #pragma unroll
+                for (int k = 0; k < NIN; ++k)
+                    yq[k] = rot ? ld16(qs + (k * RPI + rr) * D + pc) : u32x4_v{0u, 0u, 0u, 0u};
+                if (rot) {
+    #pragma unroll
+                    for (int k = 0; k < NIN; ++k) {
+                        float x[8], y[8], cs[8], sn[8];
+                        unpack8<bf16_t>(nq[k], x);
+                        unpack8<bf16_t>(yq[k], y);
+                        unpack8<bf16_t>(cw[k], cs);
+                        unpack8<bf16_t>(sw[k], sn);
+                        const float sg = 8 * c < hr ? -1.0f : 1.0f;
+                        u32x4_v o;
+    #pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            o[j] = cvt_pk<bf16_t>(x[2 * j] * cs[2 * j] + sg * y[2 * j] * sn[2 * j],
+                                               x[2 * j + 1] * cs[2 * j + 1] + sg * y[2 * j + 1] * sn[2 * j + 1]);
+                        st16(qs + (k * RPI + rr) * D + 8 * c, o);
+                    }
+                }
+            }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const int pc = 8 * c < hr ? 8 * c + hr : 8 * c - hr;
-            u32x4_v yq[NIN];
-#pragma unroll
-            for (int k = 0; k < NIN; ++k)
-                yq[k] = rot ? ld16(qs + (k * RPI + rr) * D + pc) : u32x4_v{0u, 0u, 0u, 0u};
-            if (rot) {
-#pragma unroll
-                for (int k = 0; k < NIN; ++k) {
-                    float x[8], y[8], cs[8], sn[8];
-                    unpack8<bf16_t>(nq[k], x);
-                    unpack8<bf16_t>(yq[k], y);
-                    unpack8<bf16_t>(cw[k], cs);
-                    unpack8<bf16_t>(sw[k], sn);
-                    const float sg = 8 * c < hr ? -1.0f : 1.0f;
-                    u32x4_v o;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        o[j] = cvt_pk<bf16_t>(x[2 * j] * cs[2 * j] + sg * y[2 * j] * sn[2 * j],
-                                           x[2 * j + 1] * cs[2 * j + 1] + sg * y[2 * j + 1] * sn[2 * j + 1]);
-                    st16(qs + (k * RPI + rr) * D + 8 * c, o);
-                }
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(ld16(qs + (lane & 15) * D + 32 * s + 8 * g4));
+    #pragma unroll
+            for (int s = 0; s < KS; ++s) qb[s] = to_op<op_t>(ld16(qs + (lane & 15) * D + 32 * s + 8 * g4));
     }
 
     f32x4_v oacc[DBK];
