@@ -39,22 +39,24 @@ std::mutex g_mixed_mu;
 std::vector<MixedStreams> g_mixed;
 
 // The library stream and fork/join events of the current device (created on
-// first use, default priority).
-const MixedStreams* mixed_streams(int device) {
+// first use, default priority), returned by value: the table may grow while
+// another device's call is using its entry.  False if they cannot be created.
+bool mixed_streams(int device, MixedStreams* out) {
     std::lock_guard<std::mutex> lock(g_mixed_mu);
-    if (device < 0) return nullptr;
+    if (device < 0) return false;
     if (static_cast<size_t>(device) >= g_mixed.size()) g_mixed.resize(device + 1);
     MixedStreams& m = g_mixed[device];
     if (!m.aux) {
         if (hipStreamCreateWithFlags(&m.aux, hipStreamNonBlocking) != hipSuccess) {
             m.aux = nullptr;
-            return nullptr;
+            return false;
         }
-        if (hipEventCreateWithFlags(&m.fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&m.join, hipEventDisableTiming) != hipSuccess)
-            return nullptr;
     }
-    return m.fork && m.join ? &m : nullptr;
+    if (!m.fork && hipEventCreateWithFlags(&m.fork, hipEventDisableTiming) != hipSuccess) m.fork = nullptr;
+    if (!m.join && hipEventCreateWithFlags(&m.join, hipEventDisableTiming) != hipSuccess) m.join = nullptr;
+    if (!m.fork || !m.join) return false;
+    *out = m;
+    return true;
 }
 
 int env_int(const char* name, int dflt) {
@@ -146,8 +148,9 @@ extern "C" int supersonic_attn_gfx950_mixed(size_t device_ordinal, void* stream,
         claims = static_cast<unsigned*>(device_workspace(dev, kClaimBytes, kWorkspaceMixed));
         if (!claims) return SUPERSONIC_ERR_WORKSPACE;
     }
-    const MixedStreams* ms = mixed_streams(dev);
-    if (!ms) return SUPERSONIC_ERR_LAUNCH;
+    MixedStreams streams;
+    if (!mixed_streams(dev, &streams)) return SUPERSONIC_ERR_LAUNCH;
+    const MixedStreams* ms = &streams;
     hipStream_t st = static_cast<hipStream_t>(stream);
     // The library stream starts after the work queued on `stream` so far.
     if (hipEventRecord(ms->fork, st) != hipSuccess || hipStreamWaitEvent(ms->aux, ms->fork, 0) != hipSuccess)
