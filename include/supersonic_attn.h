@@ -281,13 +281,13 @@ int supersonic_attn_gfx950_prefill(
 /* A mixed step: one prefill chunk and a batch of decode sequences of the same
  * layer in one call (no reference counterpart: the reference runs prefill and
  * decode as separate engine steps, prefill_engine.rs / decode_engine.rs; this
- * serves chunked-prefill batching).  By default the decode, then the chunk,
- * run on `stream`.  With SUPERSONIC_MIXED_DECODE_WGS = c > 0 they run at the
- * same time on disjoint CUs: the decode first on `stream`, planned for c
- * workgroups, the chunk on a library stream forked from `stream` (same
- * priority) with a dynamic item schedule, so its workgroups take the CUs the
- * decode leaves and the decode's as they free up; `stream` then waits for
- * both (measured no faster at config 5).  Results are those of
+ * serves chunked-prefill batching).  The two run at the same time on disjoint
+ * CUs: the decode first on `stream`, planned for c workgroups (one a CU), the
+ * chunk on a library stream forked from `stream` (same priority) with a
+ * dynamic item schedule, so its workgroups take the CUs the decode leaves and
+ * the decode's as they free up; `stream` then waits for both.  c comes from
+ * the two parts' estimated times; SUPERSONIC_MIXED_DECODE_WGS sets it, and 0
+ * runs the decode, then the chunk, on `stream`.  Results are those of
  * supersonic_attn_gfx950_decode and supersonic_attn_gfx950_prefill with the
  * same arguments (the layer arguments are shared).  Either part may be empty
  * (batch 0 / chunk_len 0).  The chunk's and the decodes' cache views may

@@ -1,25 +1,23 @@
 // Mixed step: one prefill chunk and a batch of decodes of the same layer in
-// one call.
+// one call, run at the same time on disjoint compute units.
 //
-// Default: the decode, then the chunk, on the caller's stream.  Optional
-// (SUPERSONIC_MIXED_DECODE_WGS = c > 0): the two on disjoint compute units at
-// the same time.  Neither kernel fits beside the other on a CU (the prefill
-// workgroup takes 133 KB of LDS and three waves a SIMD at ~168 registers; a
-// decode wave up to 256 registers), so the split is by CU:
+// The decode is HBM-bound and the chunk MFMA-bound, so back to back each
+// leaves the other's resource idle.  Neither kernel fits beside the other on
+// a CU (the prefill workgroup takes 133 KB of LDS and three waves a SIMD at
+// ~168 registers; a decode wave up to 256 registers), so the split is by CU:
 //   1. the decode goes first on the caller's stream, planned for c
-//      workgroups, and occupies about c CUs;
+//      workgroups (one a CU), and occupies about c CUs;
 //   2. the chunk's staging kernel and the prefill kernel go on a library
 //      stream forked from the caller's; the prefill grid is the whole GPU on
-//      the dynamic item schedule (items claimed longest first from a
-//      counter), so the workgroups that find a free CU start at once and the
-//      rest as the decode's CUs free up, taking only what is left;
+//      the dynamic item schedule (items claimed longest first, each as the
+//      previous one nears its end), so the workgroups that find a free CU
+//      start at once and the rest as the decode's CUs free up, taking only
+//      what is left;
 //   3. the caller's stream waits for the library stream.
 // Launch order keeps the decode's CUs its own: its workgroups are dispatched
-// before the prefill's are enqueued.  Measured at config 5 (8192-token chunk,
-// 32 decodes of U[512, 65536] tokens) the split is no faster than the
-// default (c = 128-384: 0.82-0.85 ms against 0.83 ms; c = 32-96: 0.94-1.75
-// ms): a 4-wave decode workgroup streams only 20-40 GB/s, so the decode
-// needs nearly every CU's loads in flight to reach its HBM rate.
+// before the prefill's are enqueued.  c comes from the two parts' estimated
+// times (mixed_decode_wgs); SUPERSONIC_MIXED_DECODE_WGS sets it (0: the two
+// one after the other on the caller's stream).
 #include <algorithm>
 #include <mutex>
 #include <vector>
@@ -65,6 +63,30 @@ int env_int(const char* name, int dflt) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// Decode workgroups of the CU split: c = n_cu * clamp(0.25 + 0.9 r, 0.5,
+// 0.875) rounded to a multiple of 32, r = t_d / (t_d + t_p), with the decode's
+// time t_d estimated as its K/V bytes at 6.4 TB/s (sequence lengths taken as
+// max_kv_len / 2 on average; the lengths themselves are in device memory) and
+// the chunk's t_p as its causal flops at 1.0 PF/s.  The decode on c CUs runs
+// slower than its share of the GPU would suggest (each workgroup's loads in
+// flight bound its rate), so c sits above the time share.  Fitted on config-5
+// shapes, 16/2 heads, D 256 (one MI355X; c = 96..224 swept): 32 decodes of
+// U[512, 65536] + an 8192-token chunk best at 160, 16 decodes + 8192 at 128,
+// 8 + 8192 at 128, 32 + a 4096-token chunk at 224, the values this picks.
+int mixed_decode_wgs(int n_cu, bool fp8, size_t Hq, size_t Hkv, size_t D, const supersonic_prefill_chunk* c,
+                     const supersonic_decode_batch* d) {
+    const double esz = fp8 ? 1.0 + 4.0 / static_cast<double>(D) : 2.0;  // + the per-token scales
+    const double bytes = static_cast<double>(d->batch) * (0.5 * static_cast<double>(d->max_kv_len)) * 2.0 *
+                         static_cast<double>(Hkv) * static_cast<double>(D) * esz;
+    const double S = static_cast<double>(c->chunk_len), L0 = static_cast<double>(c->chunk_start);
+    const double flops = 4.0 * static_cast<double>(Hq) * static_cast<double>(D) * S * (L0 + 0.5 * (S + 1.0));
+    const double td = bytes / 6.4e12, tp = flops / 1.0e15;
+    const double r = td / std::max(td + tp, 1e-12);
+    const double f = std::min(0.875, std::max(0.5, 0.25 + 0.9 * r));
+    const int w = (static_cast<int>(f * n_cu + 16.0) / 32) * 32;
+    return std::max(32, std::min(w, n_cu));
+}
 
 
 }  // namespace
@@ -120,8 +142,13 @@ extern "C" int supersonic_attn_gfx950_mixed(size_t device_ordinal, void* stream,
         }
     }
     if (!has_c && !has_d) return 0;
-    const int wgs = env_int("SUPERSONIC_MIXED_DECODE_WGS", 0);  // 0: one after the other
-    if (has_c && has_d && wgs <= 0) {
+    int wgs = env_int("SUPERSONIC_MIXED_DECODE_WGS", -1);  // unset: from the estimate; 0: one after the other
+    if (has_c && has_d && wgs < 0) {
+        int n_cu = device_cu_count(dev);
+        if (n_cu <= 0) n_cu = 256;
+        wgs = mixed_decode_wgs(n_cu, kv_dtype == SUPERSONIC_KV_FP8_E4M3, q_heads, kv_heads, head_dim, chunk, decode);
+    }
+    if (has_c && has_d && wgs == 0) {
         const int rc = decode_native(device_ordinal, stream, kv_dtype, decode->batch, q_heads, kv_heads, head_dim,
                                      rotary_dim, decode->max_kv_len, eps, scale, decode->q_proj, decode->k_new,
                                      decode->v_new, q_norm_w, k_norm_w, cos_table, sin_table, decode->positions,

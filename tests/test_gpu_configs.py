@@ -94,9 +94,10 @@ def test_config5_mixed_paged_batch(mode, monkeypatch):
     holding an 8192-token prefill chunk (offset 0) and 32 decode sequences with
     the benchmark's lengths (seed 5, U[512, 65536]), both checked against the
     oracle.  serial: prefill then decode on one stream.  concurrent: one mixed
-    call with the CU split (decode planned for 96 workgroups, the chunk on a
-    second stream with the dynamic schedule), made twice on a caller
-    workspace: the second call gives the same chunk output bit for bit and
+    call with the CU split (the decode planned for the estimate's workgroups
+    (160 here), the chunk on a second stream with the dynamic schedule), made
+    twice on a caller workspace, the second time with the decode on 96
+    workgroups: the second call gives the same chunk output bit for bit and
     leaves the claim counters at zero."""
     Hq, Hkv, D, rot, ps, S = 16, 2, 256, 64, 64, 8192
     lens = torch.randint(512, 65537, (32,), generator=torch.Generator().manual_seed(5)).tolist()
@@ -164,7 +165,7 @@ def test_config5_mixed_paged_batch(mode, monkeypatch):
         dec = {"q_proj": args_d["q_proj"], "k_new": args_d["k_new"], "v_new": args_d["v_new"],
                "positions": args_d["pos"], "cache": dec_cache, "out": out_d, "max_kv_len": max(lens) + 1}
         ws = torch.zeros(K.mixed_workspace_size(False, Hq, Hkv, D, chunk, dec), dtype=torch.uint8, device=DEV)
-        monkeypatch.setenv("SUPERSONIC_MIXED_DECODE_WGS", "96")
+        monkeypatch.delenv("SUPERSONIC_MIXED_DECODE_WGS", raising=False)
         K.fused_mixed(0, qw_d, kw_d, cos_d, sin_d, chunk=chunk, decode=dec, q_heads=Hq, kv_heads=Hkv, head_dim=D,
                       rotary_dim=rot, stream=st, workspace=ws)
         st.synchronize()
@@ -172,6 +173,7 @@ def test_config5_mixed_paged_batch(mode, monkeypatch):
         first_c = out_c.clone()
         first_d = out_d.clone()
         out_c.fill_(float("nan"))
+        monkeypatch.setenv("SUPERSONIC_MIXED_DECODE_WGS", "96")
         K.fused_mixed(0, qw_d, kw_d, cos_d, sin_d, chunk=chunk, decode=dec, q_heads=Hq, kv_heads=Hkv, head_dim=D,
                       rotary_dim=rot, stream=st, workspace=ws)
         st.synchronize()

@@ -1,9 +1,9 @@
 """supersonic_attn_gfx950_mixed: a prefill chunk and a decode batch of one layer in
-one call, in its default mode (decode, then chunk, on the caller's stream) and its
-CU-split mode (SUPERSONIC_MIXED_DECODE_WGS: the decode planned for fewer
-workgroups, the chunk on a second stream with the dynamic item schedule), each
-checked against the oracle.  The config-5 full-size case lives in
-test_gpu_configs.py."""
+one call, with the CU split (the decode planned for fewer workgroups, the chunk on
+a second stream with the dynamic item schedule; its workgroup count from the
+estimate or set by SUPERSONIC_MIXED_DECODE_WGS) and one after the other
+(SUPERSONIC_MIXED_DECODE_WGS=0), each checked against the oracle.  The config-5
+full-size case lives in test_gpu_configs.py."""
 import pytest
 import torch
 
@@ -21,14 +21,16 @@ def _deq(q, sc):
 
 
 @pytest.mark.parametrize("fp8", [False, True])
-@pytest.mark.parametrize("split_wgs", [0, 24])
+@pytest.mark.parametrize("split_wgs", [None, "0", "24"])
 def test_mixed_matches_oracle(fp8, split_wgs, monkeypatch):
     """A 200-token chunk after a 130-token prefix (8/2 heads, D 128, rotary 32) and
     5 ragged decodes share the layer weights and one call; the chunk's sequence
     and the decodes have their own caches.  Checked against the oracle's prefill
     and decode steps, including the appended K/V (V bit for bit)."""
-    if split_wgs:
-        monkeypatch.setenv("SUPERSONIC_MIXED_DECODE_WGS", str(split_wgs))
+    if split_wgs is None:
+        monkeypatch.delenv("SUPERSONIC_MIXED_DECODE_WGS", raising=False)
+    else:
+        monkeypatch.setenv("SUPERSONIC_MIXED_DECODE_WGS", split_wgs)
     Hq, Hkv, D, rot, S, start = 8, 2, 128, 32, 200, 130
     lens = [37, 300, 1, 1000, 513]
     B = len(lens)
@@ -95,13 +97,14 @@ def test_mixed_matches_oracle(fp8, split_wgs, monkeypatch):
         assert torch.equal(chunk_cache.v[0, :, start:start + S].float().cpu(), vch)
 
 
-def test_mixed_one_part_matches_the_single_calls():
+def test_mixed_one_part_matches_the_single_calls(monkeypatch):
     """A mixed call with an empty decode batch is the prefill call, and one with an
     empty chunk the decode call (same outputs bit for bit; the decode under
     SUPERSONIC_DECODE_DETERMINISTIC, whose split order is fixed)."""
     import os
     Hq, Hkv, D, rot, S = 8, 2, 128, 32, 150
     announce("mixed with one part empty")
+    monkeypatch.delenv("SUPERSONIC_MIXED_DECODE_WGS", raising=False)
     g = gen(83)
     qp = O.randn_bf16(g, S, Hq * 2 * D).to(DEV)
     kn = O.randn_bf16(g, S, Hkv * D).to(DEV)
