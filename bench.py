@@ -6,8 +6,8 @@ Headline (``value``): BASELINE config 2, the Qwen3.5-9B decode attention at
 32k context, batch 8: one *step* is one ``supersonic_attn_gfx950_decode`` call
 (QK RMSNorm + partial RoPE + KV append + split-K attention + LSE merge +
 sigmoid gate) for all 8 sequences.  ``value`` is algorithmic bytes per step
-(K+V of 32768 cached tokens per sequence, plus q, gate and out
-section 2) / measured time per step, in GB/s.  Inputs are synthetic N(0,1)
+(K+V of 32768 cached tokens per sequence, plus q, gate and out) / measured
+time per step, in GB/s.  Inputs are synthetic N(0,1)
 tensors resident in HBM before the timed region; the KV caches (1.07 GB) are
 larger than the 256 MB last-level cache, so every step streams HBM.
 
@@ -61,7 +61,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", args.gpus))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the attention hot path is "
-                                   "single-GPU (how it would shard is described in DESIGN.md); "
+                                   "single-GPU; "
                                    f"got --gpus {args.gpus}"}))
         sys.exit(2)
 
