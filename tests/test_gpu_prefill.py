@@ -121,6 +121,9 @@ def run_fused_prefill(c, chunk_start, cache):
 
 @pytest.mark.parametrize("S,Hq,Hkv,D,rot,start", [
     (512, 16, 4, 256, 64, 0), (200, 8, 2, 128, 32, 0), (333, 16, 4, 256, 64, 700), (64, 4, 1, 64, 32, 3),
+    # rotary halves of 48 (the LDS-staged prologue), 64, 128 (operand-layout
+    # prologue, partner chunks 2 and 4 apart) and a full-width rotation at D 128
+    (160, 4, 1, 256, 96, 50), (160, 4, 1, 256, 128, 50), (130, 8, 2, 256, 256, 17), (96, 4, 2, 128, 128, 0),
 ])
 def test_fused_prefill_matches_oracle(S, Hq, Hkv, D, rot, start):
     announce(f"fused prefill S={S} Hq={Hq} Hkv={Hkv} D={D} start={start}")
