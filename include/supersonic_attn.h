@@ -295,7 +295,9 @@ int supersonic_attn_gfx950_prefill(
  * (library-owned) or caller device memory of at least
  * supersonic_attn_gfx950_mixed_workspace_size() bytes, zero-filled before its
  * first use and not written between calls.  Calls sharing the library
- * stream of a device must not overlap. */
+ * stream of a device must not overlap.  The library stream and its two events
+ * are created by the first CU-split call on a device: make that call outside
+ * stream capture (later calls can be captured with a caller workspace). */
 typedef struct supersonic_prefill_chunk {
     size_t chunk_len;
     size_t chunk_start;
