@@ -1,6 +1,7 @@
 """A whole decode layer (input norm + Q/K/V projections, fused attention step,
-output projection + residual) and a fused prefill chunk captured into a HIP
-graph through torch.cuda.CUDAGraph.  The entry points allocate nothing once
+output projection + residual), a fused prefill chunk and a mixed call (two
+streams forked and joined inside the capture) captured into a HIP graph
+through torch.cuda.CUDAGraph.  The entry points allocate nothing once
 their workspaces exist and record no memset nodes.  The prefill is
 deterministic, so its replays equal the eager result bit for bit; the decode
 waves claim 16-token blocks dynamically, so the fp32 order of their merge and
@@ -216,3 +217,63 @@ def test_first_call_captured_with_caller_workspaces():
         assert_close_ulps(hidden, e_hidden, f"replay {r}: hidden", floor=2.0 ** -6)
         assert torch.equal(pout, e_pout), f"replay {r}: prefill"
         assert int(ws["dec"][:65536].count_nonzero()) == 0
+
+
+def test_mixed_call_graph_replays_match_eager(monkeypatch):
+    """A mixed call in its CU-split mode (the decode on 32 workgroups from the
+    capturing stream, the chunk on the library stream, forked and joined by
+    events) captured after one eager call (which creates the library stream),
+    on a caller workspace: every replay gives the eager chunk output bit for bit
+    and the decode under SUPERSONIC_DECODE_DETERMINISTIC bit for bit, and the
+    claim counters are back at zero after each replay."""
+    monkeypatch.setenv("SUPERSONIC_MIXED_DECODE_WGS", "32")
+    monkeypatch.setenv("SUPERSONIC_DECODE_DETERMINISTIC", "1")
+    Hq, Hkv, D, rot, S, start = 8, 2, 128, 32, 300, 64
+    lens = [700, 33, 1500]
+    announce("mixed call graph")
+    g = gen(95)
+    qw, kw = (t.to(DEV) for t in O.norm_weights(g, D))
+    cos, sin = (t.to(DEV) for t in O.rope_tables(rot, 2000, 1.0e7))
+    kc = torch.zeros(1, Hkv, start + S, D, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kc[0, :, :start] = O.randn_bf16(g, Hkv, start, D)
+    vc[0, :, :start] = O.randn_bf16(g, Hkv, start, D)
+    kc0, vc0 = kc.to(DEV), vc.to(DEV)
+    dk0 = O.randn_bf16(g, len(lens), Hkv, 1600, D).to(DEV)
+    dv0 = O.randn_bf16(g, len(lens), Hkv, 1600, D).to(DEV)
+    chunk_cache = K.KvCache(kc0.clone(), vc0.clone())
+    dec_cache = K.KvCache(dk0.clone(), dv0.clone())
+    out_c = torch.empty(S, Hq * D, dtype=torch.bfloat16, device=DEV)
+    out_d = torch.empty(len(lens), Hq * D, dtype=torch.bfloat16, device=DEV)
+    chunk = {"q_proj": O.randn_bf16(g, S, Hq * 2 * D).to(DEV), "k_new": O.randn_bf16(g, S, Hkv * D).to(DEV),
+             "v_new": O.randn_bf16(g, S, Hkv * D).to(DEV), "cache": chunk_cache, "out": out_c, "chunk_start": start}
+    dec = {"q_proj": O.randn_bf16(g, len(lens), Hq * 2 * D).to(DEV),
+           "k_new": O.randn_bf16(g, len(lens), Hkv * D).to(DEV), "v_new": O.randn_bf16(g, len(lens), Hkv * D).to(DEV),
+           "positions": torch.tensor(lens, dtype=torch.int32, device=DEV), "cache": dec_cache, "out": out_d,
+           "max_kv_len": max(lens) + 1}
+    ws = torch.zeros(K.mixed_workspace_size(False, Hq, Hkv, D, chunk, dec), dtype=torch.uint8, device=DEV)
+    s = torch.cuda.Stream()
+
+    def call():
+        K.fused_mixed(0, qw, kw, cos, sin, chunk=chunk, decode=dec, q_heads=Hq, kv_heads=Hkv, head_dim=D,
+                      rotary_dim=rot, stream=s, workspace=ws)
+    torch.cuda.synchronize()
+    call()  # eager (creates the library stream)
+    s.synchronize()
+    eager_c, eager_d = out_c.clone(), out_d.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        call()
+    for r in range(3):
+        out_c.zero_()
+        out_d.zero_()
+        chunk_cache.k.copy_(kc0)
+        chunk_cache.v.copy_(vc0)
+        dec_cache.k.copy_(dk0)
+        dec_cache.v.copy_(dv0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_c, eager_c), f"replay {r}: chunk"
+        assert torch.equal(out_d, eager_d), f"replay {r}: decodes"
+        assert int(ws[:2048].count_nonzero()) == 0, f"replay {r}: claim counters"
