@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
-    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|prefill_fp8|fp8|mixed|qkv|qkv_rope|oproj|layer_graph|copy")
+    ap.add_argument("--only", default="", help="run one workload: decode8|decode_cfg1|decode1|prefill|prefill_fp8|fp8|mixed|qkv|qkv_rope|oproj|layer_graph|copy|read")
     return ap.parse_args()
 
 
@@ -105,7 +105,8 @@ def main():
         out["cpu_baseline"] = W.cpu_decode8()
     if not args.skip_extra:
         out["extra"] = {k: getattr(W, k)() for k in ("decode_cfg1", "decode1", "prefill", "prefill_fp8", "fp8", "mixed",
-                                                          "qkv", "qkv_rope", "oproj", "proj_gemm", "prefill_layer", "layer_graph")}
+                                                          "qkv", "qkv_rope", "oproj", "proj_gemm", "prefill_layer", "layer_graph",
+                                                          "read")}
     print(json.dumps(out))
 
 
@@ -671,6 +672,35 @@ class Workloads:
             b.copy_(a)
         torch.cuda.synchronize()
         return {"workload": "copy", "bytes": n}
+
+    def read(self):
+        """Plain streaming reads of each decode config's byte count, for scale
+        next to the decode legs: torch's int64 sum over a device buffer of that
+        size (rotating over copies so that no read is served by the 256 MB
+        MALL), median of 20 timed reads, and the same bytes over the decode
+        leg's kernel time would read at that rate."""
+        torch = self.torch
+        out = {}
+        for name, nbytes in (("decode_cfg1", 4198400), ("decode1", 134225920), ("fp8", 305144352),
+                             ("decode8", 1073807360)):
+            copies = max(1, min(8, (512 << 20) // nbytes + 1))
+            bufs = [torch.ones(nbytes // 8, dtype=torch.int64, device=self.dev) for _ in range(copies)]
+            for i in range(5):
+                bufs[i % copies].sum()
+            torch.cuda.synchronize()
+            ts = []
+            for i in range(20):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                bufs[i % copies].sum()
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            ms = statistics.median(ts)
+            out[name] = {"bytes": nbytes, "ms": round(ms, 5), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+            del bufs
+            torch.cuda.empty_cache()
+        return {"workload": "plain streaming reads (torch int64 sum) of each decode leg's bytes", **out}
 
     def cpu_decode8(self):
         """The torch fp32 oracle on this host's cores: one config-2 B=8 step."""
