@@ -287,15 +287,39 @@ class Workloads:
         keys = sum(min(start + p + 1, start + S) for p in range(S)) if start else S * (S + 1) // 2
         return 4 * Hq * D * keys
 
+    def sdpa_reference_ms(self, S, Hq, Hkv, D):
+        """torch's own causal scaled_dot_product_attention (its flash-attention
+        backend on this build) on the same shape, attention only (no norm, RoPE or
+        gate), median of 10: a reference point, never part of the library."""
+        torch = self.torch
+        q = self.randn(1, Hq, S, D, seed=70)
+        k = self.randn(1, Hkv, S, D, seed=71).repeat_interleave(Hq // Hkv, 1)
+        v = self.randn(1, Hkv, S, D, seed=72).repeat_interleave(Hq // Hkv, 1)
+        f = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            f()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return statistics.median(ts)
+
     def prefill(self):
         S, Hq, Hkv, D, rot = 4096, 16, 4, 256, 64
         step = self.prefill_case(S, Hq, Hkv, D, rot)
         step_ms, kern_ms, _ = self.timed(step)
         fl = self.causal_flops(S, Hq, D)
         ach = fl / (kern_ms * 1e-3) / 1e12
+        sdpa_ms = self.sdpa_reference_ms(S, Hq, Hkv, D)
         return {"workload": "config 3, causal prefill S=4096, 16/4 heads, D=256, fused norm/RoPE/gate",
                 "tflops_step": fl / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms, "kernel_ms": kern_ms,
-                "flops": fl,
+                "flops": fl, "torch_sdpa_ms": round(sdpa_ms, 4),
+                "torch_sdpa_tflops": round(fl / (sdpa_ms * 1e-3) / 1e12, 1),
                 "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
                              "traffic": measured_traffic("prefill"), "kernel": "prefill_kernel"}}
