@@ -34,13 +34,20 @@ constexpr int kGCpr = kGBK / 8;                     // 16-byte chunks a row
 constexpr int kGRowsPer256 = 256 / kGRowB;          // rows that share the 64 banks
 constexpr int kGSwzShift = kGRowsPer256 == 4 ? 2 : 1;
 constexpr int kGCopyRows = 1024 / kGRowB;           // rows one copy instruction moves
-constexpr int kGCopies = kGBM / kGCopyRows / 8;     // copy instructions a wave issues per operand tile
-constexpr int kGThreads = 512;
+#ifndef SSA_GEMM_WAVES
+#define SSA_GEMM_WAVES 8
+#endif
+constexpr int kGWaves = SSA_GEMM_WAVES;             // 8: 2 x 4 waves of 128 x 64; 4: 2 x 2 waves of 128 x 128
+constexpr int kGWN = kGWaves / 2;                   // waves along n
+constexpr int kGWTN = kGBN / kGWN;                  // wave tile columns
+constexpr int kGJB = kGWTN / 32;                    // 32-column blocks a wave
+constexpr int kGCopies = kGBM / kGCopyRows / kGWaves;  // copy instructions a wave issues per operand tile
+constexpr int kGThreads = 64 * kGWaves;
 constexpr int kGTileBytes = kGBM * kGBK * 2;        // 16 KB: one operand tile
 constexpr int kGStageBytes = 2 * kGTileBytes;       // a + w
 constexpr int kGBand = 4;                           // m-tiles per band of the tile order (4: o_proj +2.5% over 8)
-constexpr int kGEpiRow = 144;                       // epilogue LDS row: 64 bf16 + 16 bytes
-constexpr int kGLds = kGStages * kGStageBytes > 8 * 128 * kGEpiRow ? kGStages * kGStageBytes : 8 * 128 * kGEpiRow;
+constexpr int kGEpiRow = 2 * kGWTN + 16;            // epilogue LDS row: a wave tile row of bf16 + 16 bytes
+constexpr int kGLds = kGStages * kGStageBytes > kGWaves * 128 * kGEpiRow ? kGStages * kGStageBytes : kGWaves * 128 * kGEpiRow;
 
 struct GemmKParams {
     const uint16_t* a;
@@ -137,12 +144,12 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     };
 
     // ---- accumulators: block (ib, jb) of this wave's 128 x 64
-    const int wm = wave >> 2, wn = wave & 3;
-    f32x16_v acc[4][2];
+    const int wm = wave / kGWN, wn = wave % kGWN;
+    f32x16_v acc[4][kGJB];
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
+        for (int jb = 0; jb < kGJB; ++jb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[ib][jb][e] = 0.f;
 
@@ -151,7 +158,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     const int orow = lane & 31;
     const int sw_x = (orow >> kGSwzShift) % kGCpr;
     const int a_rd = (wm * 128 + orow) * kGRowB;
-    const int w_rd = (wn * 64 + orow) * kGRowB;
+    const int w_rd = (wn * kGWTN + orow) * kGRowB;
 
     // Wait until tile kt has landed in LDS (this wave's copies, then every
     // wave's through the barrier); tile kt + 3 then goes to the stage of tile
@@ -167,7 +174,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
         if (kt + kGStages - 1 < KT) issue(kt + kGStages - 1);
     };
     // Fragments of k16 step s of tile kt, and the 16 MFMAs of one step.
-    auto read_frags = [&](int kt, int s, bf16x8_v (&af)[4], bf16x8_v (&bfr)[2]) {
+    auto read_frags = [&](int kt, int s, bf16x8_v (&af)[4], bf16x8_v (&bfr)[kGJB]) {
         const uint8_t* sa = lds + ((kt - kt0) % kGStages) * kGStageBytes;
         const uint8_t* sw = sa + kGTileBytes;
         const int ck = (2 * s + (lane >> 5)) ^ sw_x;
@@ -175,14 +182,14 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
         for (int ib = 0; ib < 4; ++ib)
             af[ib] = *reinterpret_cast<const bf16x8_v*>(sa + a_rd + ib * 32 * kGRowB + ck * 16);
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
+        for (int jb = 0; jb < kGJB; ++jb)
             bfr[jb] = *reinterpret_cast<const bf16x8_v*>(sw + w_rd + jb * 32 * kGRowB + ck * 16);
     };
-    auto mma_step = [&](const bf16x8_v (&af)[4], const bf16x8_v (&bfr)[2]) {
+    auto mma_step = [&](const bf16x8_v (&af)[4], const bf16x8_v (&bfr)[kGJB]) {
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-            for (int jb = 0; jb < 2; ++jb)
+            for (int jb = 0; jb < kGJB; ++jb)
                 acc[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ib], bfr[jb], acc[ib][jb], 0, 0, 0);
     };
 #pragma unroll
@@ -190,7 +197,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
         if (kt0 + u < KT) issue(kt0 + u);
     // Software pipeline over the k16 steps: the fragments of the next step
     // are read while the MFMAs of the current one run (two register sets).
-    bf16x8_v a0[4], b0[2], a1[4], b1[2];
+    bf16x8_v a0[4], b0[kGJB], a1[4], b1[kGJB];
     if (kt0 < KT) {
         arrive_tile(kt0);
         read_frags(kt0, 0, a0, b0);
@@ -200,9 +207,9 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             bf16x8_v(&ca)[4] = (st & 1) ? a1 : a0;
-            bf16x8_v(&cb)[2] = (st & 1) ? b1 : b0;
+            bf16x8_v(&cb)[kGJB] = (st & 1) ? b1 : b0;
             bf16x8_v(&na)[4] = (st & 1) ? a0 : a1;
-            bf16x8_v(&nb)[2] = (st & 1) ? b0 : b1;
+            bf16x8_v(&nb)[kGJB] = (st & 1) ? b0 : b1;
             if (st + 1 < NS) {
                 read_frags(kt, st + 1, na, nb);
             } else if (kt + 1 < KT) {
@@ -227,17 +234,17 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     // late producer's bump evens the counts, and the next call waits for its
     // own producer again.
     if (is_tail) {
-        uint32_t* pt = p.part + ((static_cast<int64_t>(tj >> 1) * 8 + wave) * 32) * 64 * 4;
+        uint32_t* pt = p.part + ((static_cast<int64_t>(tj >> 1) * kGWaves + wave) * (16 * kGJB)) * 64 * 4;
         unsigned* produced = p.flags + 2 * (tj >> 1);
         unsigned* consumed = produced + 1;
         if (!half) {
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-                for (int jb = 0; jb < 2; ++jb)
+                for (int jb = 0; jb < kGJB; ++jb)
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
-                        const int rr = (ib * 2 + jb) * 4 + qd;
+                        const int rr = (ib * kGJB + jb) * 4 + qd;
                         u32x4_v v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] = __float_as_uint(acc[ib][jb][4 * qd + e]);
@@ -278,10 +285,10 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-                for (int jb = 0; jb < 2; ++jb)
+                for (int jb = 0; jb < kGJB; ++jb)
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
-                        const int rr = (ib * 2 + jb) * 4 + qd;
+                        const int rr = (ib * kGJB + jb) * 4 + qd;
                         const u32x4_v v = ld_coh<4>(pt + rr * 64 * 4, lane * 16);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) acc[ib][jb][4 * qd + e] += __uint_as_float(v[e]);
@@ -300,7 +307,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
+        for (int jb = 0; jb < kGJB; ++jb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int r = ib * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
@@ -313,11 +320,12 @@ __global__ __launch_bounds__(kGThreads) void gemm_bt_kernel(GemmKParams p) {
     void* outp = pick3(p.out, seg);
     const bool vec = (p.vec_mask >> seg) & 1;  // ns % 8 == 0 and 16-byte aligned rows
     const int64_t obase = b * p.o_bs;
+    constexpr int kCpr = kGWTN / 8;  // 16-byte chunks of a wave tile row
 #pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < 128 * kCpr / 64; ++it) {
         const int qd = it * 64 + lane;
-        const int r = qd >> 3, c = qd & 7;
-        const int row = m0 + wm * 128 + r, col = n0 + wn * 64 + 8 * c;
+        const int r = qd / kCpr, c = qd % kCpr;
+        const int row = m0 + wm * 128 + r, col = n0 + wn * kGWTN + 8 * c;
         if (row >= p.m || col >= ns) continue;
         const u32x4_v v = *reinterpret_cast<const u32x4_v*>(blk + r * kGEpiRow + c * 16);
         const int64_t o = obase + static_cast<int64_t>(row) * ns + col;
