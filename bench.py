@@ -378,8 +378,11 @@ class Workloads:
         4096-token cached prefix (Qwen3.5-9B shape, 16/4 heads, D 256).  The prefix
         is read as codes x scale (bf16), the chunk unquantised; the chunk's K/V are
         appended as e4m3 codes + scales.  Roofline of the MFMA attention kernel;
-        stage_ms = the rest of the step (the K/V staging pass: norm + RoPE + append
-        of the chunk, dequantised prefix K and V^T)."""
+        stage_ms = the step time minus the attention kernel's event-pair time,
+        which come from two passes: besides the K/V staging pass (norm + RoPE +
+        append of the chunk, dequantised prefix K and V^T) it carries the
+        difference in the long MFMA kernel's clock between the passes (several
+        per cent), so rocprof's time of kv_stage_kernel is the staging's own."""
         torch, K = self.torch, self.K
         S, start, Hq, Hkv, D, rot = 4096, 4096, 16, 4, 256, 64
         L = start + S
